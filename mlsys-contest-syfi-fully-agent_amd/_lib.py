@@ -1,0 +1,80 @@
+"""ctypes bindings of the package's HIP libraries (built by build.py into lib/).
+
+Loading fails loudly when a library is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(_DIR, "lib")
+MOE_LIB = os.path.join(LIB_DIR, "libmoe_fp8_ds.so")
+SYNTH_LIB = os.path.join(LIB_DIR, "libmoe_synth.so")
+
+# moe_fp8_ds_status (include/moe_fp8_ds.h)
+OK, ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP, ERR_ARG = 0, -1, -2, -3, -4, -5, -6
+
+
+class Layout(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in
+                ("topk_ids", "topk_w", "pair_row", "expert_off", "perm_token", "act", "down", "sync", "total")]
+
+
+_moe = None
+_synth = None
+
+
+def _need(path: str) -> None:
+    if not os.path.exists(path):
+        raise RuntimeError(f"HIP library missing: {path}; build it with __graft_entry__.build() "
+                           f"or python mlsys-contest-syfi-fully-agent_amd/build.py")
+
+
+def moe_lib() -> ctypes.CDLL:
+    global _moe
+    if _moe is None:
+        _need(MOE_LIB)
+        L = ctypes.CDLL(MOE_LIB)
+        P, i64, sz, dbl = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t, ctypes.c_double
+        L.moe_fp8_ds_version.restype = ctypes.c_int
+        L.moe_fp8_ds_status_string.argtypes, L.moe_fp8_ds_status_string.restype = [ctypes.c_int], ctypes.c_char_p
+        L.moe_fp8_ds_max_tokens.restype = i64
+        L.moe_fp8_ds_workspace_size.argtypes, L.moe_fp8_ds_workspace_size.restype = [i64], sz
+        L.moe_fp8_ds_workspace_layout.argtypes = [i64, ctypes.POINTER(Layout)]
+        L.moe_fp8_ds_workspace_layout.restype = ctypes.c_int
+        L.moe_fp8_ds_run.argtypes = [P, P, P, P, P, P, P, P, i64, dbl, P, i64, P, sz, P]
+        L.moe_fp8_ds_run.restype = ctypes.c_int
+        L.moe_fp8_ds_route.argtypes = [P, P, i64, dbl, i64, P, sz, P]
+        L.moe_fp8_ds_route.restype = ctypes.c_int
+        _moe = L
+    return _moe
+
+
+def synth_lib() -> ctypes.CDLL:
+    global _synth
+    if _synth is None:
+        _need(SYNTH_LIB)
+        L = ctypes.CDLL(SYNTH_LIB)
+        P, i64, u64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int
+        L.moe_synth_logits.argtypes = [u64, i64, P, P]
+        L.moe_synth_bias.argtypes = [u64, P, i32, ctypes.c_float, P, P]
+        L.moe_synth_hidden.argtypes = [u64, i64, P, P, P]
+        L.moe_synth_w13.argtypes = [u64, i32, i32, P, P, P]
+        L.moe_synth_w2.argtypes = [u64, i32, i32, P, P, P]
+        for f in ("moe_synth_logits", "moe_synth_bias", "moe_synth_hidden", "moe_synth_w13", "moe_synth_w2"):
+            getattr(L, f).restype = ctypes.c_int
+        _synth = L
+    return _synth
+
+
+def status_string(rc: int) -> str:
+    return moe_lib().moe_fp8_ds_status_string(rc).decode()
+
+
+def layout(T: int) -> Layout:
+    lay = Layout()
+    rc = moe_lib().moe_fp8_ds_workspace_layout(T, ctypes.byref(lay))
+    if rc != OK:
+        raise ValueError(f"moe_fp8_ds_workspace_layout({T}): {status_string(rc)}")
+    return lay

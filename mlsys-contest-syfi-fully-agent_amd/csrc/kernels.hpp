@@ -1,0 +1,16 @@
+// kernels.hpp -- launchers of the device stages (one per .hip file).
+#pragma once
+
+#include "moe_common.hpp"
+
+namespace moe {
+
+hipError_t launch_route(const float* logits, const uint16_t* bias, float rsf, int T, int64_t offset,
+                        const Layout& L, char* ws, hipStream_t stream);
+hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
+                        const float* w13_scale, const Layout& L, char* ws, hipStream_t stream);
+hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
+                        hipStream_t stream);
+hipError_t launch_combine(int T, const Layout& L, char* ws, void* out, hipStream_t stream);
+
+}  // namespace moe

@@ -1,0 +1,114 @@
+// moe_api.cpp -- the C ABI (include/moe_fp8_ds.h): argument validation,
+// workspace layout and the stream-ordered launch sequence.
+//
+// Replaces the reference host path run_impl (moe/solution/cuda/moe.cu:2650-2896):
+// no lazily grown global workspace (the caller owns it), no default-stream use
+// (the caller's stream), no host synchronisation at any T (the device builds
+// the expert schedule), and status codes instead of unchecked CUDA calls.
+#include <cmath>
+
+#include "../../include/moe_fp8_ds.h"
+#include "kernels.hpp"
+
+namespace {
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_common(int64_t T, void* workspace, size_t workspace_bytes, double rsf) {
+  if (T < 0 || T > moe::kMaxTokens) return MOE_FP8_DS_ERR_SHAPE;
+  if (!std::isfinite(rsf)) return MOE_FP8_DS_ERR_ARG;
+  if (T == 0) return MOE_FP8_DS_OK;
+  if (!workspace) return MOE_FP8_DS_ERR_NULL;
+  if (!aligned16(workspace)) return MOE_FP8_DS_ERR_ALIGN;
+  if (workspace_bytes < moe::make_layout(T).total) return MOE_FP8_DS_ERR_WORKSPACE;
+  return MOE_FP8_DS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_fp8_ds_version(void) { return MOE_FP8_DS_VERSION; }
+
+const char* moe_fp8_ds_status_string(int status) {
+  switch (status) {
+    case MOE_FP8_DS_OK: return "ok";
+    case MOE_FP8_DS_ERR_NULL: return "null pointer argument";
+    case MOE_FP8_DS_ERR_SHAPE: return "token count out of range";
+    case MOE_FP8_DS_ERR_ALIGN: return "pointer not 16-byte aligned";
+    case MOE_FP8_DS_ERR_WORKSPACE: return "workspace too small";
+    case MOE_FP8_DS_ERR_HIP: return "HIP launch failed";
+    case MOE_FP8_DS_ERR_ARG: return "invalid scalar argument";
+    default: return "unknown status";
+  }
+}
+
+int64_t moe_fp8_ds_max_tokens(void) { return moe::kMaxTokens; }
+
+size_t moe_fp8_ds_workspace_size(int64_t T) {
+  if (T < 0 || T > moe::kMaxTokens) return 0;
+  return moe::make_layout(T).total;
+}
+
+int moe_fp8_ds_workspace_layout(int64_t T, moe_fp8_ds_layout* out) {
+  if (!out) return MOE_FP8_DS_ERR_NULL;
+  if (T < 0 || T > moe::kMaxTokens) return MOE_FP8_DS_ERR_SHAPE;
+  const moe::Layout L = moe::make_layout(T);
+  out->topk_ids = L.topk_ids;
+  out->topk_w = L.topk_w;
+  out->pair_row = L.pair_row;
+  out->expert_off = L.expert_off;
+  out->perm_token = L.perm_token;
+  out->act = L.act;
+  out->down = L.down;
+  out->sync = L.sync;
+  out->total = L.total;
+  return MOE_FP8_DS_OK;
+}
+
+int moe_fp8_ds_route(const float* routing_logits, const void* routing_bias,
+                     int64_t local_expert_offset, double routed_scaling_factor, int64_t T,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int rc = check_common(T, workspace, workspace_bytes, routed_scaling_factor);
+  if (rc != MOE_FP8_DS_OK || T == 0) return rc;
+  if (!routing_logits || !routing_bias) return MOE_FP8_DS_ERR_NULL;
+  if (!aligned16(routing_logits)) return MOE_FP8_DS_ERR_ALIGN;
+  const moe::Layout L = moe::make_layout(T);
+  hipError_t err = moe::launch_route(routing_logits, (const uint16_t*)routing_bias,
+                                     (float)routed_scaling_factor, (int)T, local_expert_offset, L,
+                                     (char*)workspace, stream);
+  return err == hipSuccess ? MOE_FP8_DS_OK : MOE_FP8_DS_ERR_HIP;
+}
+
+int moe_fp8_ds_run(const float* routing_logits, const void* routing_bias, const void* hidden_states,
+                   const float* hidden_states_scale, const void* gemm1_weights,
+                   const float* gemm1_weights_scale, const void* gemm2_weights,
+                   const float* gemm2_weights_scale, int64_t local_expert_offset,
+                   double routed_scaling_factor, void* output, int64_t T, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
+  int rc = check_common(T, workspace, workspace_bytes, routed_scaling_factor);
+  if (rc != MOE_FP8_DS_OK || T == 0) return rc;
+  const void* ptrs[] = {routing_logits, routing_bias,        hidden_states,  hidden_states_scale,
+                        gemm1_weights,  gemm1_weights_scale, gemm2_weights,  gemm2_weights_scale,
+                        output};
+  for (const void* p : ptrs)
+    if (!p) return MOE_FP8_DS_ERR_NULL;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return MOE_FP8_DS_ERR_ALIGN;
+
+  const moe::Layout L = moe::make_layout(T);
+  char* ws = (char*)workspace;
+  const int t = (int)T;
+  hipError_t err = moe::launch_route(routing_logits, (const uint16_t*)routing_bias,
+                                     (float)routed_scaling_factor, t, local_expert_offset, L, ws,
+                                     stream);
+  if (err == hipSuccess)
+    err = moe::launch_gemm1((const uint8_t*)hidden_states, hidden_states_scale, t,
+                            (const uint8_t*)gemm1_weights, gemm1_weights_scale, L, ws, stream);
+  if (err == hipSuccess)
+    err = moe::launch_gemm2(t, (const uint8_t*)gemm2_weights, gemm2_weights_scale, L, ws, stream);
+  if (err == hipSuccess) err = moe::launch_combine(t, L, ws, output, stream);
+  return err == hipSuccess ? MOE_FP8_DS_OK : MOE_FP8_DS_ERR_HIP;
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+// moe_common.hpp -- shared constants, workspace layout and device helpers of
+// the gfx950 FP8 block-scale MoE layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace moe {
+
+// Geometry fixed by the definition (moe.py:65-76; moe.cu:39-51).
+constexpr int kH = 7168;          // hidden size
+constexpr int kI = 2048;          // intermediate size
+constexpr int k2I = 4096;         // gate + up
+constexpr int kELocal = 32;       // local experts
+constexpr int kEGlobal = 256;     // global experts
+constexpr int kTopK = 8;
+constexpr int kNGroup = 8;
+constexpr int kTopKGroup = 4;
+constexpr int kGroupSize = 32;
+constexpr int kBlk = 128;         // quantisation block
+constexpr int kNHBlk = kH / kBlk;   // 56
+constexpr int kNIBlk = kI / kBlk;   // 16
+constexpr int kN2IBlk = k2I / kBlk; // 32
+constexpr int kWave = 64;
+
+// Largest T any entry point accepts: keeps every row index (< 8T) and every
+// grid dimension inside int32 / HIP limits.
+constexpr int64_t kMaxTokens = 1 << 20;
+
+// Indices inside the workspace's int32 `sync` region.
+constexpr int kSyncRouteDone = 0;  // route blocks finished (last one resets it)
+
+struct Layout {
+  size_t topk_ids, topk_w, pair_row, expert_off, perm_token, act, down, sync, total;
+};
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+inline Layout make_layout(int64_t T) {
+  Layout L{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = align_up(off + bytes, 256);
+    return at;
+  };
+  const size_t rows = (size_t)T * kTopK;  // upper bound on routed local pairs
+  L.sync = take(64 * sizeof(int32_t));
+  L.expert_off = take(64 * sizeof(int32_t));
+  L.topk_ids = take(rows * sizeof(int32_t));
+  L.topk_w = take(rows * sizeof(float));
+  L.pair_row = take(rows * sizeof(int32_t));
+  L.perm_token = take(rows * sizeof(int32_t));
+  L.act = take(rows * kI * sizeof(uint16_t));
+  L.down = take(rows * kH * sizeof(float));
+  L.total = off;
+  return L;
+}
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+
+// Order-preserving map of a (non-NaN) float to uint32.
+__device__ __forceinline__ uint32_t float_order_key(float v) {
+  uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float float_from_order_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = __shfl_xor(lo, mask, kWave);
+  hi = __shfl_xor(hi, mask, kWave);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t u64max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// D = A(16x128 e4m3) * B(128x16 e4m3), fp32 16x16 result (no accumulate-in).
+// Lane l supplies 32 K-bytes of row (l % 16) of A and of column (l % 16) of
+// B; lanes l/16 = 0..3 cover the four 32-byte quarters of the 128 K values.
+// Output: lane l holds rows 4*(l/16)+i, column l % 16, i = 0..3.
+__device__ __forceinline__ v4f mfma_f8_16x16x128(const v8i& a, const v8i& b) {
+  v4f z = {0.f, 0.f, 0.f, 0.f};
+  // Format codes 0/0 = e4m3 for both operands; zero scale operands select
+  // the unscaled v_mfma_f32_16x16x128_f8f6f4.
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
+}
+
+// D = C + A(16x32 bf16) * B(32x16 bf16): lane l supplies 8 K-values of row
+// (l % 16) of A / column (l % 16) of B at K = 8*(l/16) .. +8.
+__device__ __forceinline__ v4f mfma_bf16_16x16x32(const v8bf& a, const v8bf& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 8 e4m3 bytes (two dwords) -> 8 bf16 (exact: every e4m3 value is a bf16).
+__device__ __forceinline__ v8bf e4m3x8_to_bf16(uint32_t lo, uint32_t hi) {
+  v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+  v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+  v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+  v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+  v8bf r;
+  r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+  r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+  return r;
+}
+
+// Row m-tile lookup shared by the grouped GEMMs: global tile index `tile` ->
+// (local expert, first row, rows in tile) given the expert row offsets
+// off[0..32] and tile height bm.  Returns false past the last real tile.
+__device__ __forceinline__ bool find_row_tile(const int32_t* __restrict__ off, int tile, int bm,
+                                              int& expert, int& row0, int& rows) {
+  int acc = 0;
+#pragma unroll 1
+  for (int e = 0; e < kELocal; ++e) {
+    const int n = off[e + 1] - off[e];
+    const int tl = (n + bm - 1) / bm;
+    if (tile < acc + tl) {
+      expert = e;
+      row0 = off[e] + (tile - acc) * bm;
+      rows = min(bm, off[e + 1] - row0);
+      return true;
+    }
+    acc += tl;
+  }
+  return false;
+}
+
+}  // namespace moe

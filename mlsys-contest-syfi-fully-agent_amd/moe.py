@@ -1,0 +1,135 @@
+"""Python entry point of the gfx950 FP8 MoE layer, mirroring the contest
+solution's operator `run` (moe/solution/cuda/moe.cu:2650-2661, exported at
+moe.cu:2898 as "moe.cu::run", destination-passing style per moe/config.toml:6-11).
+
+    run(routing_logits, routing_bias, hidden_states, hidden_states_scale,
+        gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale,
+        local_expert_offset, routed_scaling_factor, output)
+
+Arguments have the names, order, dtypes and shapes of the definition
+(full-agent-pipeline/references/moe.py:29-40, shape checks moe.py:71-91); the
+result is written into `output` ([T, 7168] bf16), which is also returned.
+Shape and dtype mismatches raise AssertionError like the reference's asserts;
+a failing HIP call raises RuntimeError.  The work is enqueued on the current
+HIP stream of the tensors' device; nothing synchronises the host.
+
+All arithmetic happens in libmoe_fp8_ds.so (HIP kernels for gfx950); this file
+only checks arguments, owns the per-device workspace and passes pointers.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import torch
+
+from . import _lib
+
+H, I, E_LOCAL, E_GLOBAL, TOP_K, BLOCK = 7168, 2048, 32, 256, 8, 128
+
+_ws_lock = threading.Lock()
+_ws: dict = {}
+
+
+def workspace(device: torch.device, T: int) -> torch.Tensor:
+    """Zero-initialised per-device workspace, grown on demand."""
+    need = _lib.moe_lib().moe_fp8_ds_workspace_size(T)
+    key = (device.type, device.index)
+    with _ws_lock:
+        buf = _ws.get(key)
+        if buf is None or buf.numel() < need:
+            buf = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+            _ws[key] = buf
+        return buf
+
+
+def _ptr(t: torch.Tensor):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _check(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+           gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output=None) -> int:
+    T = routing_logits.shape[0]
+    f8 = torch.float8_e4m3fn
+    assert routing_logits.dtype == torch.float32 and routing_logits.shape == (T, E_GLOBAL)
+    assert routing_bias.dtype == torch.bfloat16 and routing_bias.shape[-1] == E_GLOBAL
+    assert routing_bias.numel() == E_GLOBAL
+    if hidden_states is not None:
+        assert hidden_states.dtype == f8 and hidden_states.shape == (T, H)
+        assert hidden_states_scale.dtype == torch.float32 and hidden_states_scale.shape == (H // BLOCK, T)
+        assert gemm1_weights.dtype == f8 and gemm1_weights.shape == (E_LOCAL, 2 * I, H)
+        assert gemm1_weights_scale.dtype == torch.float32
+        assert gemm1_weights_scale.shape == (E_LOCAL, 2 * I // BLOCK, H // BLOCK)
+        assert gemm2_weights.dtype == f8 and gemm2_weights.shape == (E_LOCAL, H, I)
+        assert gemm2_weights_scale.dtype == torch.float32
+        assert gemm2_weights_scale.shape == (E_LOCAL, H // BLOCK, I // BLOCK)
+    if output is not None:
+        assert output.dtype == torch.bfloat16 and output.shape == (T, H)
+    dev = routing_logits.device
+    tensors = [routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+               gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output]
+    for t in tensors:
+        if t is None:
+            continue
+        assert t.device == dev, "all tensors must be on the same device"
+        assert t.is_contiguous(), "all tensors must be contiguous"
+    if dev.type != "cuda":
+        raise RuntimeError("moe_fp8_ds runs on a ROCm GPU only (no CPU path)")
+    return T
+
+
+def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+        gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+        routed_scaling_factor, output):
+    T = _check(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+               gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
+    dev = routing_logits.device
+    ws = workspace(dev, T)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = _lib.moe_lib().moe_fp8_ds_run(
+        _ptr(routing_logits), _ptr(routing_bias), _ptr(hidden_states), _ptr(hidden_states_scale),
+        _ptr(gemm1_weights), _ptr(gemm1_weights_scale), _ptr(gemm2_weights), _ptr(gemm2_weights_scale),
+        int(local_expert_offset), float(routed_scaling_factor), _ptr(output), T, _ptr(ws), ws.numel(),
+        ctypes.c_void_p(stream))
+    if rc != _lib.OK:
+        raise RuntimeError(f"moe_fp8_ds_run: {_lib.status_string(rc)} ({rc})")
+    return output
+
+
+class RouteResult:
+    """Typed views of the routing/permutation regions of a workspace."""
+
+    def __init__(self, ws: torch.Tensor, T: int):
+        lay = _lib.layout(T)
+
+        def view(off, n, dtype):
+            nbytes = n * torch.empty((), dtype=dtype).element_size()
+            return ws[off:off + nbytes].view(dtype)
+
+        self.topk_ids = view(lay.topk_ids, T * TOP_K, torch.int32).view(T, TOP_K)
+        self.topk_w = view(lay.topk_w, T * TOP_K, torch.float32).view(T, TOP_K)
+        self.pair_row = view(lay.pair_row, T * TOP_K, torch.int32).view(T, TOP_K)
+        self.expert_off = view(lay.expert_off, E_LOCAL + 1, torch.int32)
+        self.perm_token = view(lay.perm_token, T * TOP_K, torch.int32)
+        self.act = view(lay.act, T * TOP_K * I, torch.int16).view(T * TOP_K, I)
+        self.down = view(lay.down, T * TOP_K * H, torch.float32).view(T * TOP_K, H)
+        self.sync = view(lay.sync, 64, torch.int32)
+
+
+def route(routing_logits, routing_bias, local_expert_offset, routed_scaling_factor, ws=None):
+    """Routing + permutation only; returns typed views into the workspace."""
+    T = _check(routing_logits, routing_bias, None, None, None, None, None, None)
+    dev = routing_logits.device
+    ws = workspace(dev, T) if ws is None else ws
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = _lib.moe_lib().moe_fp8_ds_route(_ptr(routing_logits), _ptr(routing_bias), int(local_expert_offset),
+                                         float(routed_scaling_factor), T, _ptr(ws), ws.numel(),
+                                         ctypes.c_void_p(stream))
+    if rc != _lib.OK:
+        raise RuntimeError(f"moe_fp8_ds_route: {_lib.status_string(rc)} ({rc})")
+    return RouteResult(ws, T)
+
+
+def intermediates(ws: torch.Tensor, T: int) -> RouteResult:
+    """Views of every intermediate region after a `run` call for T tokens."""
+    return RouteResult(ws, T)

@@ -1,0 +1,145 @@
+"""GPU parity of the whole layer (route -> GEMM1+SwiGLU -> GEMM2 -> combine)
+against the CPU oracle and against the reference's own golden output rows,
+through the C ABI (bf16 output within atol = rtol = 1e-2)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+from util import bf16_close, gpu_tokens, gpu_weights, near_tie_tokens, oracle_inputs
+
+pytestmark = pytest.mark.gpu
+
+H, I = 7168, 2048
+
+
+def run_layer(pkg, tok, w, off, rsf, fill=float("nan")):
+    T = tok[0].shape[0]
+    out = torch.full((T, H), fill, dtype=torch.bfloat16, device=tok[0].device)
+    pkg.run(*tok, *w, off, rsf, out)
+    torch.cuda.synchronize()
+    return out
+
+
+def sample_tokens(ids, off, n, rng, T):
+    """Up to n tokens with at least one local expert, plus two without."""
+    le = ids - off
+    has = ((le >= 0) & (le < 32)).any(axis=1)
+    loc = np.nonzero(has)[0]
+    non = np.nonzero(~has)[0]
+    pick = list(rng.choice(loc, size=min(n, loc.size), replace=False)) if loc.size else []
+    pick += list(non[:2])
+    return np.array(sorted(pick), np.int64)
+
+
+LAYER_CASES = [
+    ("plumbing_t16", None, None, 16),
+    ("decode_t1", None, None, 1),
+    ("decode_t1_s3", None, None, 1),
+    ("small_t64", None, None, 64),
+    ("prefill_t1024", None, None, 40),
+    ("skewed_t8192", None, None, 24),
+    ("small_t64", 224, None, 64),
+    ("small_t64", 240, 37, 37),
+    ("small_t64", -16, 21, 21),
+    ("prefill_t1024", 256, 128, 8),
+]
+
+
+@pytest.mark.parametrize("name,offset,T,n_check", LAYER_CASES)
+def test_layer_matches_oracle(pkg, orc, cuda_device, name, offset, T, n_check):
+    cfg = pkg.synth.CONFIGS[name]
+    off = cfg.local_expert_offset if offset is None else offset
+    w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, host = gpu_tokens(pkg, cfg, cuda_device, T)
+    T = tok[0].shape[0]
+    print(f"layer case {name} offset={off} T={T}", flush=True)
+    out = run_layer(pkg, tok, w, off, cfg.routed_scaling_factor).float().cpu().numpy()
+    assert np.isfinite(out).all(), "output not fully written / non-finite"
+
+    ref_ids, _ = orc.route(host[0], host[1], cfg.routed_scaling_factor)
+    tie = near_tie_tokens(host[0], host[1], cfg.routed_scaling_factor)
+    rng = np.random.default_rng(T)
+    toks = np.arange(T) if T <= n_check else sample_tokens(ref_ids, off, n_check, rng, T)
+    toks = toks[~tie[toks]]
+    x = oracle_inputs(cfg, host, w_host)
+    ref = orc.bf16_to_f32(orc.moe(x, tokens=toks, local_expert_offset=off))
+    got = out[toks]
+    bad = bf16_close(got, ref)
+    err = np.abs(got - ref)
+    print(f"  checked {len(toks)} tokens: max|err| {err.max():.3e}, max|ref| {np.abs(ref).max():.3f}")
+    assert not bad.any(), f"{int(bad.sum())} elements outside tolerance, worst {err.max()}"
+    # tokens without a local expert produce exact zeros
+    le = ref_ids - off
+    none = np.nonzero(~((le >= 0) & (le < 32)).any(axis=1))[0]
+    assert (out[none] == 0).all()
+
+
+@pytest.mark.parametrize("name", ["plumbing_t16", "small_t64", "prefill_t1024"])
+def test_layer_matches_reference_golden(pkg, cuda_device, name):
+    """Compare with bf16 rows written by the reference moe.py itself."""
+    g = load_golden(f"out_{name}.npz")
+    cfg = pkg.synth.CONFIGS[name]
+    w, _ = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, _ = gpu_tokens(pkg, cfg, cuda_device)
+    out = run_layer(pkg, tok, w, cfg.local_expert_offset, cfg.routed_scaling_factor)
+    got = out.float().cpu().numpy()
+    ref = (g["out"].astype(np.uint32) << 16).view(np.float32)
+    bad = bf16_close(got[g["rows"]], ref)
+    assert not bad.any(), f"{int(bad.sum())} elements outside tolerance"
+    nz = np.nonzero(np.abs(got).sum(axis=1) > 0)[0]
+    np.testing.assert_array_equal(nz, g["nonzero_rows"])
+
+
+def test_intermediates_match_oracle(pkg, orc, cuda_device):
+    """SwiGLU activation rows (bf16) and GEMM2 rows (fp32) per (token, expert) pair."""
+    cfg = pkg.synth.CONFIGS["small_t64"]
+    w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, host = gpu_tokens(pkg, cfg, cuda_device)
+    T = tok[0].shape[0]
+    run_layer(pkg, tok, w, cfg.local_expert_offset, cfg.routed_scaling_factor)
+    r = pkg.intermediates(pkg.workspace(cuda_device, T), T)
+    offs = r.expert_off.cpu().numpy()
+    n = int(offs[32])
+    perm = r.perm_token.cpu().numpy()[:n]
+    le = np.searchsorted(offs, np.arange(n), side="right") - 1
+    act = (r.act[:n].cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    down = r.down[:n].cpu().numpy()
+    x = oracle_inputs(cfg, host, w_host)
+    c_ref, o_ref = orc.expert_rows(x, perm, le)
+    assert not bf16_close(act, c_ref, atol=1e-3, rtol=1e-2).any()
+    assert not bf16_close(down, o_ref, atol=1e-2, rtol=1e-2).any()
+
+
+def test_zero_tokens_is_noop(pkg, cuda_device):
+    cfg = pkg.synth.CONFIGS["plumbing_t16"]
+    w, _ = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, _ = gpu_tokens(pkg, cfg, cuda_device, 0)
+    out = torch.empty((0, H), dtype=torch.bfloat16, device=cuda_device)
+    pkg.run(*tok, *w, 0, 2.5, out)
+    torch.cuda.synchronize()
+
+
+def test_layer_deterministic(pkg, cuda_device):
+    cfg = pkg.synth.CONFIGS["prefill_t1024"]
+    w, _ = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, _ = gpu_tokens(pkg, cfg, cuda_device)
+    a = run_layer(pkg, tok, w, 0, 2.5)
+    b = run_layer(pkg, tok, w, 0, 2.5, fill=0.0)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_synth_matches_cpu_generator(pkg, orc, cuda_device):
+    """The GPU generator writes the same bytes as the oracle's CPU generator."""
+    for name in ("plumbing_t16", "skewed_t8192"):
+        cfg = pkg.synth.CONFIGS[name]
+        _, host = gpu_tokens(pkg, cfg, cuda_device, 64)
+        ref = orc.make_tokens(orc.CONFIGS[name], 64)
+        for a, b in zip(host, ref):
+            np.testing.assert_array_equal(a, b)
+    _, w_host = gpu_weights(pkg, 0, cuda_device)
+    ref = orc.make_weights(0, (0, 2))
+    np.testing.assert_array_equal(w_host[0][:2], ref[0][:2])
+    np.testing.assert_array_equal(w_host[1][:2], ref[1][:2])
+    np.testing.assert_array_equal(w_host[2][:2], ref[2][:2])
+    np.testing.assert_array_equal(w_host[3][:2], ref[3][:2])
