@@ -79,6 +79,23 @@ int moe_fp8_ds_run(const float* routing_logits, const void* routing_bias,
                    int64_t local_expert_offset, double routed_scaling_factor, void* output,
                    int64_t T, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Number of device stages of moe_fp8_ds_run: routing + permutation, GEMM1 +
+ * SwiGLU, GEMM2, combine. */
+#define MOE_FP8_DS_NUM_STAGES 4
+
+/* moe_fp8_ds_run, plus a hipEventRecord on `stream` before the first stage and
+ * after each stage: stage_events[0..MOE_FP8_DS_NUM_STAGES], all created by the
+ * caller (timing-enabled).  Elapsed time between events i and i+1 is stage i.
+ * Instrumentation for benchmarks; it has no counterpart in the reference
+ * (whose harness times only the whole call, moe/scripts/run_local.py:33). */
+int moe_fp8_ds_run_profiled(const float* routing_logits, const void* routing_bias,
+                            const void* hidden_states, const float* hidden_states_scale,
+                            const void* gemm1_weights, const float* gemm1_weights_scale,
+                            const void* gemm2_weights, const float* gemm2_weights_scale,
+                            int64_t local_expert_offset, double routed_scaling_factor, void* output,
+                            int64_t T, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                            hipEvent_t* stage_events);
+
 /* Routing and permutation only (moe.py:123-158 and the per-expert token lists
  * of moe.py:168-179; moe.cu route_kernel :60-186, scan :217-283, perm_fill
  * :288-309).  Fills the workspace regions described by

@@ -35,6 +35,8 @@ def moe_lib() -> ctypes.CDLL:
     global _moe
     if _moe is None:
         _need(MOE_LIB)
+        import torch  # noqa: F401  (torch's HIP runtime first: one runtime per process)
+
         L = ctypes.CDLL(MOE_LIB)
         P, i64, sz, dbl = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t, ctypes.c_double
         L.moe_fp8_ds_version.restype = ctypes.c_int
@@ -45,6 +47,8 @@ def moe_lib() -> ctypes.CDLL:
         L.moe_fp8_ds_workspace_layout.restype = ctypes.c_int
         L.moe_fp8_ds_run.argtypes = [P, P, P, P, P, P, P, P, i64, dbl, P, i64, P, sz, P]
         L.moe_fp8_ds_run.restype = ctypes.c_int
+        L.moe_fp8_ds_run_profiled.argtypes = [P, P, P, P, P, P, P, P, i64, dbl, P, i64, P, sz, P, P]
+        L.moe_fp8_ds_run_profiled.restype = ctypes.c_int
         L.moe_fp8_ds_route.argtypes = [P, P, i64, dbl, i64, P, sz, P]
         L.moe_fp8_ds_route.restype = ctypes.c_int
         _moe = L
@@ -55,6 +59,8 @@ def synth_lib() -> ctypes.CDLL:
     global _synth
     if _synth is None:
         _need(SYNTH_LIB)
+        import torch  # noqa: F401
+
         L = ctypes.CDLL(SYNTH_LIB)
         P, i64, u64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int
         L.moe_synth_logits.argtypes = [u64, i64, P, P]
@@ -78,3 +84,61 @@ def layout(T: int) -> Layout:
     if rc != OK:
         raise ValueError(f"moe_fp8_ds_workspace_layout({T}): {status_string(rc)}")
     return lay
+
+
+_hip = None
+
+
+def hip_lib() -> ctypes.CDLL:
+    """The HIP runtime torch already loaded (imported first so that this and
+    the package's libraries bind to one runtime instance)."""
+    global _hip
+    if _hip is None:
+        import torch  # noqa: F401  (loads torch's libamdhip64.so.7)
+
+        L = ctypes.CDLL("libamdhip64.so.7")
+        P = ctypes.c_void_p
+        L.hipEventCreate.argtypes = [ctypes.POINTER(P)]
+        L.hipEventDestroy.argtypes = [P]
+        L.hipEventSynchronize.argtypes = [P]
+        L.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), P, P]
+        for f in ("hipEventCreate", "hipEventDestroy", "hipEventSynchronize", "hipEventElapsedTime"):
+            getattr(L, f).restype = ctypes.c_int
+        _hip = L
+    return _hip
+
+
+class EventPool:
+    """`n` timing-enabled hipEvents (raw handles for the C ABI)."""
+
+    def __init__(self, n: int):
+        L = hip_lib()
+        self.events = (ctypes.c_void_p * n)()
+        for i in range(n):
+            ev = ctypes.c_void_p()
+            rc = L.hipEventCreate(ctypes.byref(ev))
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreate failed ({rc})")
+            self.events[i] = ev
+        self.n = n
+
+    def ptr(self, first: int = 0):
+        """Address of events[first..] as a hipEvent_t* argument."""
+        return ctypes.c_void_p(ctypes.addressof(self.events) + first * ctypes.sizeof(ctypes.c_void_p))
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        L = hip_lib()
+        ms = ctypes.c_float()
+        rc = L.hipEventSynchronize(self.events[b])
+        if rc == 0:
+            rc = L.hipEventElapsedTime(ctypes.byref(ms), self.events[a], self.events[b])
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def close(self):
+        L = hip_lib()
+        for i in range(self.n):
+            if self.events[i]:
+                L.hipEventDestroy(self.events[i])
+                self.events[i] = None

@@ -80,12 +80,12 @@ int moe_fp8_ds_route(const float* routing_logits, const void* routing_bias,
   return err == hipSuccess ? MOE_FP8_DS_OK : MOE_FP8_DS_ERR_HIP;
 }
 
-int moe_fp8_ds_run(const float* routing_logits, const void* routing_bias, const void* hidden_states,
-                   const float* hidden_states_scale, const void* gemm1_weights,
-                   const float* gemm1_weights_scale, const void* gemm2_weights,
-                   const float* gemm2_weights_scale, int64_t local_expert_offset,
-                   double routed_scaling_factor, void* output, int64_t T, void* workspace,
-                   size_t workspace_bytes, hipStream_t stream) {
+static int run_layer(const float* routing_logits, const void* routing_bias, const void* hidden_states,
+                     const float* hidden_states_scale, const void* gemm1_weights,
+                     const float* gemm1_weights_scale, const void* gemm2_weights,
+                     const float* gemm2_weights_scale, int64_t local_expert_offset,
+                     double routed_scaling_factor, void* output, int64_t T, void* workspace,
+                     size_t workspace_bytes, hipStream_t stream, hipEvent_t* events) {
   int rc = check_common(T, workspace, workspace_bytes, routed_scaling_factor);
   if (rc != MOE_FP8_DS_OK || T == 0) return rc;
   const void* ptrs[] = {routing_logits, routing_bias,        hidden_states,  hidden_states_scale,
@@ -99,16 +99,53 @@ int moe_fp8_ds_run(const float* routing_logits, const void* routing_bias, const 
   const moe::Layout L = moe::make_layout(T);
   char* ws = (char*)workspace;
   const int t = (int)T;
-  hipError_t err = moe::launch_route(routing_logits, (const uint16_t*)routing_bias,
-                                     (float)routed_scaling_factor, t, local_expert_offset, L, ws,
-                                     stream);
+  hipError_t err = hipSuccess;
+  auto mark = [&](int i) {
+    if (events && err == hipSuccess) err = hipEventRecord(events[i], stream);
+  };
+  mark(0);
+  err = err != hipSuccess ? err
+                          : moe::launch_route(routing_logits, (const uint16_t*)routing_bias,
+                                              (float)routed_scaling_factor, t, local_expert_offset,
+                                              L, ws, stream);
+  mark(1);
   if (err == hipSuccess)
     err = moe::launch_gemm1((const uint8_t*)hidden_states, hidden_states_scale, t,
                             (const uint8_t*)gemm1_weights, gemm1_weights_scale, L, ws, stream);
+  mark(2);
   if (err == hipSuccess)
     err = moe::launch_gemm2(t, (const uint8_t*)gemm2_weights, gemm2_weights_scale, L, ws, stream);
+  mark(3);
   if (err == hipSuccess) err = moe::launch_combine(t, L, ws, output, stream);
+  mark(4);
   return err == hipSuccess ? MOE_FP8_DS_OK : MOE_FP8_DS_ERR_HIP;
+}
+
+int moe_fp8_ds_run(const float* routing_logits, const void* routing_bias, const void* hidden_states,
+                   const float* hidden_states_scale, const void* gemm1_weights,
+                   const float* gemm1_weights_scale, const void* gemm2_weights,
+                   const float* gemm2_weights_scale, int64_t local_expert_offset,
+                   double routed_scaling_factor, void* output, int64_t T, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
+  return run_layer(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                   gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+                   routed_scaling_factor, output, T, workspace, workspace_bytes, stream, nullptr);
+}
+
+int moe_fp8_ds_run_profiled(const float* routing_logits, const void* routing_bias,
+                            const void* hidden_states, const float* hidden_states_scale,
+                            const void* gemm1_weights, const float* gemm1_weights_scale,
+                            const void* gemm2_weights, const float* gemm2_weights_scale,
+                            int64_t local_expert_offset, double routed_scaling_factor, void* output,
+                            int64_t T, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                            hipEvent_t* stage_events) {
+  if (!stage_events) return MOE_FP8_DS_ERR_NULL;
+  for (int i = 0; i < MOE_FP8_DS_NUM_STAGES + 1; ++i)
+    if (!stage_events[i]) return MOE_FP8_DS_ERR_NULL;
+  return run_layer(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                   gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+                   routed_scaling_factor, output, T, workspace, workspace_bytes, stream,
+                   stage_events);
 }
 
 }  // extern "C"

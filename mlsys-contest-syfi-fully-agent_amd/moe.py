@@ -80,17 +80,23 @@ def _check(routing_logits, routing_bias, hidden_states, hidden_states_scale, gem
 
 def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
         gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
-        routed_scaling_factor, output):
+        routed_scaling_factor, output, stage_events=None):
+    """`stage_events` (optional, an _lib.EventPool slice pointer) makes the
+    call record MOE_FP8_DS_NUM_STAGES + 1 events around its device stages."""
     T = _check(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
                gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
     dev = routing_logits.device
     ws = workspace(dev, T)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    rc = _lib.moe_lib().moe_fp8_ds_run(
-        _ptr(routing_logits), _ptr(routing_bias), _ptr(hidden_states), _ptr(hidden_states_scale),
-        _ptr(gemm1_weights), _ptr(gemm1_weights_scale), _ptr(gemm2_weights), _ptr(gemm2_weights_scale),
-        int(local_expert_offset), float(routed_scaling_factor), _ptr(output), T, _ptr(ws), ws.numel(),
-        ctypes.c_void_p(stream))
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    args = (_ptr(routing_logits), _ptr(routing_bias), _ptr(hidden_states), _ptr(hidden_states_scale),
+            _ptr(gemm1_weights), _ptr(gemm1_weights_scale), _ptr(gemm2_weights), _ptr(gemm2_weights_scale),
+            int(local_expert_offset), float(routed_scaling_factor), _ptr(output), T, _ptr(ws), ws.numel(),
+            stream)
+    L = _lib.moe_lib()
+    if stage_events is None:
+        rc = L.moe_fp8_ds_run(*args)
+    else:
+        rc = L.moe_fp8_ds_run_profiled(*args, stage_events)
     if rc != _lib.OK:
         raise RuntimeError(f"moe_fp8_ds_run: {_lib.status_string(rc)} ({rc})")
     return output
