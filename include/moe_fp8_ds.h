@@ -112,7 +112,7 @@ typedef struct {
   size_t expert_off; /* int32 [33]     row offsets per local expert; [32] = N_sel */
   size_t perm_token; /* int32 [8T]     token of each permuted row                 */
   size_t act;        /* bf16  [8T, 2048] SwiGLU output rows                       */
-  size_t down;       /* float [8T, 7168] GEMM2 output rows                        */
+  size_t down;       /* bf16  [8T, 7168] GEMM2 output rows                        */
   size_t sync;       /* int32 [64]     completion counters (zero between calls)   */
   size_t total;      /* = moe_fp8_ds_workspace_size(T)                            */
 } moe_fp8_ds_layout;

@@ -19,7 +19,7 @@ namespace {
 constexpr int kCombThreads = 256;
 
 __global__ void __launch_bounds__(kCombThreads)
-combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_row,
+combine_kernel(const uint16_t* __restrict__ down, const int32_t* __restrict__ pair_row,
                const float* __restrict__ topk_w, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
   int row[kTopK];
@@ -34,11 +34,11 @@ combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_
 #pragma unroll
     for (int k = 0; k < kTopK; ++k) {
       if (row[k] < 0) continue;
-      const float4 v = *(const float4*)(down + (size_t)row[k] * kH + c);
-      a0 = a0 + v.x * w[k];
-      a1 = a1 + v.y * w[k];
-      a2 = a2 + v.z * w[k];
-      a3 = a3 + v.w * w[k];
+      const uint2 v = *(const uint2*)(down + (size_t)row[k] * kH + c);
+      a0 = a0 + bf16_to_f32((uint16_t)v.x) * w[k];
+      a1 = a1 + bf16_to_f32((uint16_t)(v.x >> 16)) * w[k];
+      a2 = a2 + bf16_to_f32((uint16_t)v.y) * w[k];
+      a3 = a3 + bf16_to_f32((uint16_t)(v.y >> 16)) * w[k];
     }
     uint2 packed;
     packed.x = (uint32_t)f32_to_bf16_rne(a0) | ((uint32_t)f32_to_bf16_rne(a1) << 16);
@@ -51,7 +51,7 @@ combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_
 
 hipError_t launch_combine(int T, const Layout& L, char* ws, void* out, hipStream_t stream) {
   hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(kCombThreads), 0, stream,
-                     (const float*)(ws + L.down), (const int32_t*)(ws + L.pair_row),
+                     (const uint16_t*)(ws + L.down), (const int32_t*)(ws + L.pair_row),
                      (const float*)(ws + L.topk_w), (uint16_t*)out);
   return hipGetLastError();
 }

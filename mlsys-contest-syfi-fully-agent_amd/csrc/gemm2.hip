@@ -20,13 +20,15 @@ namespace moe {
 namespace {
 
 constexpr int kG2Threads = 256;
+// Token count from which GEMM2 uses the LDS-tiled MFMA kernel.
+constexpr int kGemm2TiledMinTokens = 2048;
 constexpr int kG2Waves = kG2Threads / kWave;
 
 template <int MI, int NJ>
 __global__ void __launch_bounds__(kG2Threads)
 gemm2_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
              const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
-             float* __restrict__ down) {
+             uint16_t* __restrict__ down) {
   constexpr int BM = 16 * MI;
   int e, row0, rows;
   if (!find_row_tile(expert_off, blockIdx.y, BM, e, row0, rows)) return;
@@ -111,7 +113,7 @@ gemm2_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = mi * 16 + lq * 4 + i;
-        if (r < rows) down[(size_t)(row0 + r) * kH + n] = acc[mi][nj][i];
+        if (r < rows) down[(size_t)(row0 + r) * kH + n] = f32_to_bf16_rne(acc[mi][nj][i]);
       }
     }
 }
@@ -122,7 +124,175 @@ hipError_t launch_gemm2_cfg(const uint8_t* w2, const float* w2_scale, const Layo
   const dim3 grid(kH / (16 * NJ), max_tiles);
   hipLaunchKernelGGL((gemm2_kernel<MI, NJ>), grid, dim3(kG2Threads), 0, stream,
                      (const uint16_t*)(ws + L.act), w2, w2_scale,
-                     (const int32_t*)(ws + L.expert_off), (float*)(ws + L.down));
+                     (const int32_t*)(ws + L.expert_off), (uint16_t*)(ws + L.down));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Tiled path (many rows per expert): LDS-staged bf16 MFMA.
+//
+//   * workgroup = WM x WN waves, wave tile (16*MI) rows x (16*NJ) columns;
+//   * a pipeline stage is 64 K values: the bf16 activation rows (A) and the
+//     e4m3 W2 rows (B), copied global -> LDS by global_load_lds_dwordx4,
+//     4 LDS buffers (loads for stage s+3 in flight while stage s multiplies);
+//   * operand fragments sit in LDS in MFMA register order: an A fragment
+//     (16 rows x 64 K bf16) is two 1 KB planes, a B fragment (16 rows x 64 K
+//     e4m3) one plane; lane L = 16*q + r owns row r, K = 16q .. 16q+15 of the
+//     stage (instruction j of the stage takes K = 16q + 8j .. +7 -- the same
+//     K permutation for A and B, so the dot products are unchanged);
+//   * B is widened e4m3 -> bf16 exactly in registers (v_cvt_scalef32_pk_bf16_fp8
+//     with scale 1); P accumulates the two stages of a 128-K scale block on
+//     v_mfma_f32_16x16x32_bf16, then acc += P * w_scale[n/128, kb].
+// ---------------------------------------------------------------------------
+template <int WM, int WN, int MI, int NJ>
+struct G2Tiled {
+  static constexpr int kWaves = WM * WN;
+  static constexpr int kThreads = kWave * kWaves;
+  static constexpr int BM = 16 * MI * WM;
+  static constexpr int BN = 16 * NJ * WN;
+  static_assert(16 * NJ <= kBlk && kBlk % (16 * NJ) == 0, "a wave's columns lie in one scale block");
+  static constexpr int kNT = kH / BN;
+  static_assert(kH % BN == 0, "column tiles");
+  static constexpr int kAFrags = BM / 16;
+  static constexpr int kBFrags = BN / 16;
+  static constexpr int kBOff = kAFrags * 2048;
+  static constexpr int kStageBytes = kBOff + kBFrags * 1024;
+  static constexpr int kStages = 4;
+  static constexpr int kSteps = kI / 64;  // stages per tile (two per scale block)
+  static constexpr int kPlanes = 2 * kAFrags + kBFrags;
+  static_assert(kPlanes % kWaves == 0, "planes must split evenly over waves");
+  static constexpr int kPlanesPerWave = kPlanes / kWaves;
+  static constexpr int kGroupM = 4;
+};
+
+template <int WM, int WN, int MI, int NJ>
+__global__ void __launch_bounds__(64 * WM * WN)
+gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
+                   const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
+                   uint16_t* __restrict__ down) {
+  using C = G2Tiled<WM, WN, MI, NJ>;
+  __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes];
+
+  const int mt_total = count_row_tiles(expert_off, C::BM);
+  const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
+  if (t < 0) return;
+  int mt, nt;
+  grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
+  int e, row0, rows;
+  find_row_tile(expert_off, mt, C::BM, e, row0, rows);
+  const int n0 = nt * C::BN;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int lq = lane >> 4;
+  const int lr = lane & 15;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+
+  // per-lane DMA sources at stage 0 (byte pointers) and LDS destinations
+  const char* src[C::kPlanesPerWave];
+  int dst[C::kPlanesPerWave];
+#pragma unroll
+  for (int k = 0; k < C::kPlanesPerWave; ++k) {
+    const int plane = wave + k * C::kWaves;
+    if (plane < 2 * C::kAFrags) {
+      const int f = plane >> 1, p = plane & 1;
+      const int r = min(f * 16 + lr, rows - 1);
+      src[k] = (const char*)(act + (size_t)(row0 + r) * kI + 16 * lq + 8 * p);
+      dst[k] = f * 2048 + p * 1024;
+    } else {
+      const int f = plane - 2 * C::kAFrags;
+      src[k] = (const char*)(w2 + ((size_t)e * kH + n0 + 16 * f + lr) * kI + 16 * lq);
+      dst[k] = C::kBOff + f * 1024;
+    }
+  }
+  auto issue = [&](int s) {
+    char* base = lds + (s % C::kStages) * C::kStageBytes;
+#pragma unroll
+    for (int k = 0; k < C::kPlanesPerWave; ++k) {
+      const int step = (dst[k] < C::kBOff) ? s * 64 * 2 : s * 64;  // bytes per stage: bf16 A, e4m3 B
+      dma16(src[k] + step, base + dst[k]);
+    }
+  };
+  const float* sb_ptr = w2_scale + ((size_t)e * kNHBlk + (n0 + 16 * NJ * wn) / kBlk) * kNIBlk;
+
+  v4f acc[MI][NJ], P[MI][NJ];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = P[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s = 0; s < C::kStages - 1; ++s) issue(s);
+#pragma unroll 1
+  for (int s = 0; s < C::kSteps; ++s) {
+    // stages s+1 .. s+kStages-2 may stay in flight
+    const int ahead = min(C::kSteps - 1 - s, C::kStages - 2);
+    if (ahead >= 2)
+      wait_vmcnt_lgkm0<2 * C::kPlanesPerWave>();
+    else if (ahead == 1)
+      wait_vmcnt_lgkm0<C::kPlanesPerWave>();
+    else
+      wait_vmcnt_lgkm0<0>();
+    block_barrier();
+    if (s + C::kStages - 1 < C::kSteps) issue(s + C::kStages - 1);
+
+    const char* sbuf = lds + (s % C::kStages) * C::kStageBytes;
+    v8bf a[MI][2], b[NJ][2];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+      const char* f = sbuf + (wm * MI + mi) * 2048 + lane * 16;
+      a[mi][0] = *(const v8bf*)f;
+      a[mi][1] = *(const v8bf*)(f + 1024);
+    }
+#pragma unroll
+    for (int nj = 0; nj < NJ; ++nj) {
+      const v4i raw = *(const v4i*)(sbuf + C::kBOff + (wn * NJ + nj) * 1024 + lane * 16);
+      b[nj][0] = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
+      b[nj][1] = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
+    }
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < NJ; ++nj) {
+        P[mi][nj] = mfma_bf16_16x16x32(a[mi][0], b[nj][0], P[mi][nj]);
+        P[mi][nj] = mfma_bf16_16x16x32(a[mi][1], b[nj][1], P[mi][nj]);
+      }
+    if (s & 1) {
+      const float sb = sb_ptr[s >> 1];
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(P[mi][nj][i], sb, acc[mi][nj][i]);
+          P[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+  }
+
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NJ; ++nj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = (wm * MI + mi) * 16 + 4 * lq + i;
+        if (r < rows)
+          down[(size_t)(row0 + r) * kH + n0 + 16 * (wn * NJ + nj) + lr] = f32_to_bf16_rne(acc[mi][nj][i]);
+      }
+}
+
+template <int WM, int WN, int MI, int NJ>
+hipError_t launch_gemm2_tiled(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
+                              hipStream_t stream) {
+  using C = G2Tiled<WM, WN, MI, NJ>;
+  const int64_t pairs = (int64_t)T * kTopK;
+  const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
+  const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
+  hipLaunchKernelGGL((gemm2_tiled_kernel<WM, WN, MI, NJ>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
+                     stream, (const uint16_t*)(ws + L.act), w2, w2_scale,
+                     (const int32_t*)(ws + L.expert_off), (uint16_t*)(ws + L.down));
   return hipGetLastError();
 }
 
@@ -137,7 +307,8 @@ inline int max_row_tiles2(int T, int bm) {
 hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
                         hipStream_t stream) {
   if (T <= 8) return launch_gemm2_cfg<1, 1>(w2, w2_scale, L, ws, max_row_tiles2(T, 16), stream);
-  return launch_gemm2_cfg<4, 4>(w2, w2_scale, L, ws, max_row_tiles2(T, 64), stream);
+  if (T < kGemm2TiledMinTokens) return launch_gemm2_cfg<4, 4>(w2, w2_scale, L, ws, max_row_tiles2(T, 64), stream);
+  return launch_gemm2_tiled<2, 4, 4, 4>(T, w2, w2_scale, L, ws, stream);
 }
 
 }  // namespace moe

@@ -53,7 +53,7 @@ inline Layout make_layout(int64_t T) {
   L.pair_row = take(rows * sizeof(int32_t));
   L.perm_token = take(rows * sizeof(int32_t));
   L.act = take(rows * kI * sizeof(uint16_t));
-  L.down = take(rows * kH * sizeof(float));
+  L.down = take(rows * kH * sizeof(uint16_t));
   L.total = off;
   return L;
 }
@@ -122,6 +122,69 @@ __device__ __forceinline__ v8bf e4m3x8_to_bf16(uint32_t lo, uint32_t hi) {
   r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
   r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
   return r;
+}
+
+// ---------------------------------------------------------------------------
+// LDS staging helpers
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Asynchronous global -> LDS copy (global_load_lds_dwordx4): lane i writes its
+// 16 bytes at lds_wave_base + 16 * i.  lds_wave_base must be wave-uniform.
+__device__ __forceinline__ void dma16(const void* g, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_wave_base, 16, 0, 0);
+}
+// Same with 4 bytes per lane (global_load_lds_dword): lane i -> base + 4 * i.
+__device__ __forceinline__ void dma4(const void* g, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_wave_base, 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0): at most N vector-memory operations of this
+// wave (loads and LDS DMA, completed in issue order) still outstanding, and
+// every LDS access of this wave complete.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+}
+
+// Workgroup barrier that the compiler may not move memory accesses across.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Number of row tiles of height bm over all local experts.
+__device__ __forceinline__ int count_row_tiles(const int32_t* __restrict__ off, int bm) {
+  int n = 0;
+#pragma unroll 1
+  for (int e = 0; e < kELocal; ++e) n += (off[e + 1] - off[e] + bm - 1) / bm;
+  return n;
+}
+
+// XCD-aware block -> tile map.  Workgroups are dispatched round-robin over the
+// 8 XCDs (block b runs on XCD b % 8), so block b takes tile
+//   (b % 8) * ceil(R / 8) + b / 8
+// of the R real tiles: each XCD walks one contiguous run of the tile order,
+// and tiles that share operands share that XCD's L2.  Returns -1 for blocks
+// past the real tiles.
+__device__ __forceinline__ int xcd_tile(int b, int R) {
+  const int per = (R + 7) / 8;
+  const int t = (b % 8) * per + b / 8;
+  return (b < per * 8 && t < R) ? t : -1;
+}
+
+// Tile order inside the run: groups of `gm` row tiles sweep all `nt` column
+// tiles, row tile fastest, so concurrently running blocks reuse both the A
+// rows and the B columns of their group.
+__device__ __forceinline__ void grouped_tile(int t, int mt_total, int nt, int gm, int& mt, int& ntile) {
+  const int group = t / (gm * nt);
+  const int first = group * gm;
+  const int rows_in_group = min(gm, mt_total - first);
+  const int r = t - first * nt;
+  mt = first + r % rows_in_group;
+  ntile = r / rows_in_group;
 }
 
 // Row m-tile lookup shared by the grouped GEMMs: global tile index `tile` ->

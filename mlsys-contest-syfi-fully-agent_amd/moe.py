@@ -118,7 +118,7 @@ class RouteResult:
         self.expert_off = view(lay.expert_off, E_LOCAL + 1, torch.int32)
         self.perm_token = view(lay.perm_token, T * TOP_K, torch.int32)
         self.act = view(lay.act, T * TOP_K * I, torch.int16).view(T * TOP_K, I)
-        self.down = view(lay.down, T * TOP_K * H, torch.float32).view(T * TOP_K, H)
+        self.down = view(lay.down, T * TOP_K * H, torch.int16).view(T * TOP_K, H)
         self.sync = view(lay.sync, 64, torch.int32)
 
 

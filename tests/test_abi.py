@@ -45,7 +45,7 @@ def test_layout_regions_disjoint_and_aligned(pkg):
         regions = sorted([
             (lay.sync, 256), (lay.expert_off, 256), (lay.topk_ids, 32 * T), (lay.topk_w, 32 * T),
             (lay.pair_row, 32 * T), (lay.perm_token, 32 * T), (lay.act, 8 * T * 2048 * 2),
-            (lay.down, 8 * T * 7168 * 4)])
+            (lay.down, 8 * T * 7168 * 2)])
         for (a, na), (b, _) in zip(regions, regions[1:]):
             assert a % 256 == 0 and a + na <= b
         assert regions[-1][0] + regions[-1][1] <= lay.total
