@@ -61,9 +61,9 @@ const char* moe_fp8_ds_status_string(int status);
 /* Largest T accepted by the entry points. */
 int64_t moe_fp8_ds_max_tokens(void);
 
-/* Bytes of workspace `moe_fp8_ds_run` needs for T tokens.  The workspace must
- * be zero-filled once before its first use; every call leaves it reusable.
- * Replaces the reference's lazily grown process-global workspace
+/* Bytes of workspace `moe_fp8_ds_run` needs for T tokens.  The workspace needs
+ * no initialisation and carries no state between calls.  Replaces the
+ * reference's lazily grown process-global workspace
  * (moe/solution/cuda/moe.cu:2511-2589). */
 size_t moe_fp8_ds_workspace_size(int64_t T);
 
@@ -113,7 +113,7 @@ typedef struct {
   size_t perm_token; /* int32 [8T]     token of each permuted row                 */
   size_t act;        /* bf16  [8T, 2048] SwiGLU output rows                       */
   size_t down;       /* bf16  [8T, 7168] GEMM2 output rows                        */
-  size_t sync;       /* int32 [64]     completion counters (zero between calls)   */
+  size_t block_hist; /* int32 [ceil(T/16), 32] local-expert pairs per routing workgroup */
   size_t total;      /* = moe_fp8_ds_workspace_size(T)                            */
 } moe_fp8_ds_layout;
 

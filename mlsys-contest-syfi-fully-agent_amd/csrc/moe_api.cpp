@@ -61,7 +61,7 @@ int moe_fp8_ds_workspace_layout(int64_t T, moe_fp8_ds_layout* out) {
   out->perm_token = L.perm_token;
   out->act = L.act;
   out->down = L.down;
-  out->sync = L.sync;
+  out->block_hist = L.block_hist;
   out->total = L.total;
   return MOE_FP8_DS_OK;
 }

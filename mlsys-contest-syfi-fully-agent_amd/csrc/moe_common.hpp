@@ -28,11 +28,8 @@ constexpr int kWave = 64;
 // grid dimension inside int32 / HIP limits.
 constexpr int64_t kMaxTokens = 1 << 20;
 
-// Indices inside the workspace's int32 `sync` region.
-constexpr int kSyncRouteDone = 0;  // route blocks finished (last one resets it)
-
 struct Layout {
-  size_t topk_ids, topk_w, pair_row, expert_off, perm_token, act, down, sync, total;
+  size_t topk_ids, topk_w, pair_row, expert_off, perm_token, act, down, block_hist, total;
 };
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -46,7 +43,6 @@ inline Layout make_layout(int64_t T) {
     return at;
   };
   const size_t rows = (size_t)T * kTopK;  // upper bound on routed local pairs
-  L.sync = take(64 * sizeof(int32_t));
   L.expert_off = take(64 * sizeof(int32_t));
   L.topk_ids = take(rows * sizeof(int32_t));
   L.topk_w = take(rows * sizeof(float));
@@ -54,6 +50,7 @@ inline Layout make_layout(int64_t T) {
   L.perm_token = take(rows * sizeof(int32_t));
   L.act = take(rows * kI * sizeof(uint16_t));
   L.down = take(rows * kH * sizeof(uint16_t));
+  L.block_hist = take((size_t)((T + 15) / 16) * kELocal * sizeof(int32_t));
   L.total = off;
   return L;
 }

@@ -7,46 +7,90 @@
 // perm_fill_kernel (moe.cu:288-309, atomics, nondeterministic order).
 //
 // Design (gfx950, wave64):
-//   * one wavefront per token; lane l owns experts l, l+64, l+128, l+192, so a
-//     routing group of 32 experts is one half-wave in one register slot and
-//     every group reduction is a 5-step xor butterfly inside the half-wave;
+//   * one wavefront per token, 16 tokens per 1024-thread workgroup; lane l
+//     owns experts l, l+64, l+128, l+192, so a routing group of 32 experts is
+//     one half-wave in one register slot;
 //   * scores are packed into 64-bit keys (order-preserving float bits, then
 //     255 - expert) so one max-reduction gives value and lowest-index
-//     tie-break at once;
-//   * the last workgroup to finish (device-scope counter) builds the
-//     permutation: per-expert counts and ranks come from wave ballots, so rows
-//     of an expert are in ascending token order and the result is
-//     deterministic; no host round trip at any T.
+//     tie-break at once; reductions use DPP lane movements (VALU latency, no
+//     LDS round trips);
+//   * T <= 16 (decode): the single workgroup also builds the permutation, with
+//     no global atomics or fences;
+//   * larger T: each workgroup stores its local-expert histogram (plain
+//     stores, no atomics); a second kernel (one workgroup per 1024 tokens)
+//     reduces the histograms to the expert row offsets and the per-chunk bases
+//     and scatters its chunk;
+//   * ranks inside a chunk come from wave ballots, so rows of an expert are in
+//     ascending token order and the result is deterministic; no host round
+//     trip at any T.
 #include "moe_common.hpp"
 
 namespace moe {
 namespace {
 
-constexpr int kRouteTokensPerBlock = 4;  // 4 waves, one token each
-constexpr int kRouteThreads = kRouteTokensPerBlock * kWave;
+constexpr int kRouteWaves = 16;
+constexpr int kRouteThreads = kRouteWaves * kWave;
+
+// ---- DPP helpers (GFX9 controls) -------------------------------------------
+constexpr int kDppQuad1032 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kDppQuad2301 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowBcast15 = 0x142;
+constexpr int kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  // lanes outside ROW_MASK keep their own value (old = v)
+  const uint32_t l2 = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t h2 = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, CTRL, ROW_MASK, 0xF, false);
+  return ((uint64_t)h2 << 32) | l2;
+}
+
+// Maximum over each row of 16 lanes, in every lane of the row.
+__device__ __forceinline__ uint64_t row_max(uint64_t k) {
+  k = u64max(k, dpp_u64<kDppQuad1032, 0xF>(k));
+  k = u64max(k, dpp_u64<kDppQuad2301, 0xF>(k));
+  k = u64max(k, dpp_u64<kDppRowHalfMirror, 0xF>(k));
+  k = u64max(k, dpp_u64<kDppRowMirror, 0xF>(k));
+  return k;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Maxima of the two half-waves (lanes 0-31, 32-63), wave-uniform.
+__device__ __forceinline__ void halfwave_max(uint64_t k, uint64_t& m0, uint64_t& m1) {
+  k = row_max(k);
+  k = u64max(k, dpp_u64<kDppRowBcast15, 0xA>(k));  // rows 1, 3 see rows 0, 2
+  m0 = readlane_u64(k, 31);
+  m1 = readlane_u64(k, 63);
+}
+
+// Maximum over the wave, wave-uniform.
+__device__ __forceinline__ uint64_t wave_max(uint64_t k) {
+  k = row_max(k);
+  k = u64max(k, dpp_u64<kDppRowBcast15, 0xA>(k));
+  k = u64max(k, dpp_u64<kDppRowBcast31, 0xC>(k));
+  return readlane_u64(k, 63);
+}
 
 __device__ __forceinline__ uint64_t make_key(float v, int e) {
   return ((uint64_t)float_order_key(v) << 32) | (uint32_t)(255 - e);
 }
 
-__device__ __forceinline__ uint64_t halfwave_max(uint64_t k) {
-#pragma unroll
-  for (int m = 1; m < 32; m <<= 1) k = u64max(k, shfl_xor_u64(k, m));
-  return k;
-}
+__device__ __forceinline__ float key_value(uint64_t k) { return float_from_order_key((uint32_t)(k >> 32)); }
 
-__device__ __forceinline__ uint64_t wave_max(uint64_t k) {
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) k = u64max(k, shfl_xor_u64(k, m));
-  return k;
-}
-
-// Routes one token with one wavefront; lanes 0..7 write ids/weights.
+// Routes token t with one wavefront.  Returns the 8 selected ids, ascending
+// (wave-uniform), and writes ids / weights.
 __device__ void route_token(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
                             float rsf, int t, int32_t* __restrict__ ids_out,
-                            float* __restrict__ w_out) {
+                            float* __restrict__ w_out, int sel[kTopK]) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int half = lane >> 5;  // 0: lanes 0-31, 1: lanes 32-63
   float s[4];
   uint64_t key[4];
 #pragma unroll
@@ -57,25 +101,19 @@ __device__ void route_token(const float* __restrict__ logits, const uint16_t* __
     const float ex = (float)exp(-(double)x);
     s[j] = 1.0f / (1.0f + ex);
     // moe.py:128: s_with_bias = s + bias
-    const float sb = s[j] + bf16_to_f32(bias[e]);
-    key[j] = make_key(sb, e);
+    key[j] = make_key(s[j] + bf16_to_f32(bias[e]), e);
   }
   // moe.py:135-136: group score = sum of the two largest biased scores.
-  // Slot j of half h holds group 2j + h.
-  float gsc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint64_t k1 = halfwave_max(key[j]);
-    const uint64_t k2 = halfwave_max(key[j] == k1 ? 0ull : key[j]);
-    gsc[j] = float_from_order_key((uint32_t)(k1 >> 32)) + float_from_order_key((uint32_t)(k2 >> 32));
-  }
-  // Gather all 8 group scores into every lane.
+  // Slot j, half h holds group 2j + h.
   float G[kNGroup];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float other = __shfl_xor(gsc[j], 32, kWave);
-    G[2 * j] = half ? other : gsc[j];
-    G[2 * j + 1] = half ? gsc[j] : other;
+    uint64_t a0, a1, b0, b1;
+    halfwave_max(key[j], a0, a1);
+    const uint64_t own = (lane < 32) ? a0 : a1;
+    halfwave_max(key[j] == own ? 0ull : key[j], b0, b1);
+    G[2 * j] = key_value(a0) + key_value(b0);
+    G[2 * j + 1] = key_value(a1) + key_value(b1);
   }
   // moe.py:139-146: keep the top-4 groups (ties -> lower group index).
   uint32_t keep = 0;
@@ -87,21 +125,19 @@ __device__ void route_token(const float* __restrict__ logits, const uint16_t* __
     keep |= (rank < kTopKGroup ? 1u : 0u) << g;
   }
   // moe.py:149-151: top-8 experts among the kept groups.
+  const int half = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     if (!((keep >> (2 * j + half)) & 1u)) key[j] = 0ull;
-  int sel[kTopK];
 #pragma unroll
   for (int r = 0; r < kTopK; ++r) {
-    uint64_t m = u64max(u64max(key[0], key[1]), u64max(key[2], key[3]));
-    m = wave_max(m);
-    const int e = 255 - (int)(uint32_t)(m & 0xFFu);
-    sel[r] = e;
+    const uint64_t m = wave_max(u64max(u64max(key[0], key[1]), u64max(key[2], key[3])));
+    sel[r] = 255 - (int)(uint32_t)(m & 0xFFu);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (key[j] == m) key[j] = 0ull;
   }
-  // Sort the 8 ids ascending (uniform across the wave).
+  // ascending ids (wave-uniform values)
 #pragma unroll
   for (int a = 1; a < kTopK; ++a)
 #pragma unroll
@@ -120,7 +156,7 @@ __device__ void route_token(const float* __restrict__ logits, const uint16_t* __
     const int e = sel[r];
     const int j = e >> 6;
     const float mine = j == 0 ? s[0] : j == 1 ? s[1] : j == 2 ? s[2] : s[3];
-    sv[r] = __shfl(mine, e & 63, kWave);
+    sv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), e & 63));
     sum = sum + sv[r];
   }
   const float denom = sum + 1e-20f;
@@ -138,131 +174,212 @@ __device__ void route_token(const float* __restrict__ logits, const uint16_t* __
   }
 }
 
-// Local-expert bitmask of token t and the position of its first local id.
-__device__ __forceinline__ uint32_t local_mask(const int32_t* __restrict__ ids, int t,
-                                               int64_t offset, int& kfirst) {
+// Local-expert bitmask of a token's 8 ascending ids, and the slot of its first
+// local id (ids ascending => local ids occupy slots kfirst .. kfirst+popc-1).
+__device__ __forceinline__ uint32_t local_mask(const int32_t id[kTopK], int64_t offset, int& kfirst) {
   uint32_t m = 0;
   kfirst = kTopK;
 #pragma unroll
-  for (int k = 0; k < kTopK; ++k) {
-    const int64_t le = (int64_t)ids[(size_t)t * kTopK + k] - offset;
+  for (int k = kTopK - 1; k >= 0; --k) {
+    const int64_t le = (int64_t)id[k] - offset;
     if (le >= 0 && le < kELocal) {
       m |= 1u << (int)le;
-      kfirst = min(kfirst, k);
+      kfirst = k;
     }
   }
   return m;
 }
 
-// Executed by the last route workgroup: expert row offsets, permutation and
-// pair -> row map, deterministic (ascending token order inside each expert).
-__device__ void build_permutation(const int32_t* __restrict__ ids, int T, int64_t offset,
-                                  int32_t* __restrict__ pair_row, int32_t* __restrict__ expert_off,
-                                  int32_t* __restrict__ perm_token) {
-  constexpr int kWaves = kRouteThreads / kWave;
-  __shared__ int wave_cnt[kWaves][kELocal];
-  __shared__ int running[kELocal];
+// Shared memory of the permutation pass.
+struct PermShared {
+  int wave_cnt[kRouteWaves][kELocal];
+  int wave_base[kRouteWaves][kELocal];
+  int running[kELocal];  // next free row per expert
+  int total[kELocal];    // pairs per expert (all tokens)
+  int before[kELocal];   // pairs per expert in tokens before this chunk
+};
+
+// Writes expert_off (when `write_off`) and sets running[e] = expert_off[e] +
+// before[e] from the totals in shared memory.  Called by wave 0.
+__device__ __forceinline__ void expert_offsets(PermShared& sh, bool write_off, int32_t* __restrict__ expert_off) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-
-  // Pass 1: per-expert counts.  Each wave accumulates its own row.
-  if (lane < kELocal) wave_cnt[wave][lane] = 0;
-  __syncthreads();
-  for (int base = 0; base < T; base += kRouteThreads) {
-    const int t = base + threadIdx.x;
-    int kf;
-    const uint32_t m = t < T ? local_mask(ids, t, offset, kf) : 0u;
-#pragma unroll 4
-    for (int le = 0; le < kELocal; ++le) {
-      const uint64_t b = __ballot((m >> le) & 1u);
-      if (lane == 0) wave_cnt[wave][le] += __popcll(b);
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = 0;
-    for (int le = 0; le < kELocal; ++le) {
-      int n = 0;
-      for (int w = 0; w < kWaves; ++w) n += wave_cnt[w][le];
-      expert_off[le] = acc;
-      running[le] = acc;
-      acc += n;
-    }
-    expert_off[kELocal] = acc;
-  }
-  __syncthreads();
-
-  // Pass 2: ranks -> rows.
-  for (int base = 0; base < T; base += kRouteThreads) {
-    const int t = base + threadIdx.x;
-    int kf = kTopK;
-    const uint32_t m = t < T ? local_mask(ids, t, offset, kf) : 0u;
-#pragma unroll 4
-    for (int le = 0; le < kELocal; ++le) {
-      const uint64_t b = __ballot((m >> le) & 1u);
-      if (lane == 0) wave_cnt[wave][le] = __popcll(b);
-    }
-    __syncthreads();
-    // Lanes past T have m == 0: they take part in the ballots and write nothing.
-    int j = 0;  // j-th local id of this token (its ids are ascending)
-    for (int le = 0; le < kELocal; ++le) {
-      const uint64_t b = __ballot((m >> le) & 1u);
-      if ((m >> le) & 1u) {
-        int row = running[le] + __popcll(b & lt_mask);
-        for (int w = 0; w < wave; ++w) row += wave_cnt[w][le];
-        pair_row[(size_t)t * kTopK + kf + j] = row;
-        perm_token[row] = t;
-        ++j;
-      }
-    }
-    if (t < T) {
+  const int c = lane < kELocal ? sh.total[lane] : 0;
+  int incl = c;
 #pragma unroll
-      for (int k = 0; k < kTopK; ++k)
-        if (k < kf || k >= kf + j) pair_row[(size_t)t * kTopK + k] = -1;
+  for (int d = 1; d < kELocal; d <<= 1) {
+    const int v = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += v;
+  }
+  if (lane < kELocal) {
+    sh.running[lane] = incl - c + sh.before[lane];
+    if (write_off) {
+      expert_off[lane] = incl - c;
+      if (lane == kELocal - 1) expert_off[kELocal] = incl;
     }
-    __syncthreads();
-    if (threadIdx.x < kELocal) {
-      int n = 0;
-      for (int w = 0; w < kWaves; ++w) n += wave_cnt[w][threadIdx.x];
-      running[threadIdx.x] += n;
-    }
-    __syncthreads();
   }
 }
 
+// Rows of the pairs of tokens [t0, t0 + 1024): ascending token order inside
+// each expert, starting at sh.running[e].  All 1024 threads take part.
+__device__ void scatter_chunk(const int32_t* __restrict__ ids, int T, int t0, int64_t offset, PermShared& sh,
+                              int32_t* __restrict__ pair_row, int32_t* __restrict__ perm_token) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int t = t0 + threadIdx.x;
+  int kf = kTopK;
+  uint32_t m = 0;  // tokens past T have no local expert
+  if (t < T) {
+    const int4 a = *(const int4*)(ids + (size_t)t * kTopK);
+    const int4 b = *(const int4*)(ids + (size_t)t * kTopK + 4);
+    const int32_t id[kTopK] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    m = local_mask(id, offset, kf);
+  }
+  // per-expert counts of this wave: lane le keeps popc(ballot of expert le)
+  int mycnt = 0;
+#pragma unroll
+  for (int le = 0; le < kELocal; ++le) {
+    const int c = __popcll(__ballot((m >> le) & 1u));
+    if (lane == le) mycnt = c;
+  }
+  if (lane < kELocal) sh.wave_cnt[wave][lane] = mycnt;
+  __syncthreads();
+  if (threadIdx.x < kELocal) {
+    int acc = sh.running[threadIdx.x];
+#pragma unroll
+    for (int w = 0; w < kRouteWaves; ++w) {
+      sh.wave_base[w][threadIdx.x] = acc;
+      acc += sh.wave_cnt[w][threadIdx.x];
+    }
+    sh.running[threadIdx.x] = acc;
+  }
+  __syncthreads();
+  // Rows: the wave's base for the expert plus the lane's rank among the
+  // wave's lanes holding that expert (ballots again; every lane takes part).
+  int32_t row[kTopK];
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) row[k] = -1;
+  int j = kf;
+#pragma unroll
+  for (int le = 0; le < kELocal; ++le) {
+    const uint64_t b = __ballot((m >> le) & 1u);
+    if ((m >> le) & 1u) {
+      row[j] = sh.wave_base[wave][le] + __popcll(b & lt_mask);
+      ++j;
+    }
+  }
+  if (t < T) {
+    int4 r0, r1;
+    r0.x = row[0]; r0.y = row[1]; r0.z = row[2]; r0.w = row[3];
+    r1.x = row[4]; r1.y = row[5]; r1.z = row[6]; r1.w = row[7];
+    *(int4*)(pair_row + (size_t)t * kTopK) = r0;
+    *(int4*)(pair_row + (size_t)t * kTopK + 4) = r1;
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k)
+      if (row[k] >= 0) perm_token[row[k]] = t;
+  }
+  __syncthreads();  // wave_cnt / wave_base may be reused
+}
+
+// Routing of 16 tokens per workgroup.  With a single workgroup (T <= 16) it
+// also builds the permutation; otherwise it writes its local-expert histogram
+// to block_hist[blockIdx.x][32] for perm_kernel.
 __global__ void __launch_bounds__(kRouteThreads)
 route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf, int T,
              int64_t offset, int32_t* __restrict__ ids, float* __restrict__ w,
              int32_t* __restrict__ pair_row, int32_t* __restrict__ expert_off,
-             int32_t* __restrict__ perm_token, int32_t* __restrict__ sync) {
-  const int t = blockIdx.x * kRouteTokensPerBlock + threadIdx.x / kWave;
-  if (t < T) route_token(logits, bias, rsf, t, ids, w);
-
-  // Completion count; the last block builds the permutation.
-  __shared__ int is_last;
-  __threadfence();
+             int32_t* __restrict__ perm_token, int32_t* __restrict__ block_hist) {
+  __shared__ int hist[kELocal];
+  if (threadIdx.x < kELocal) hist[threadIdx.x] = 0;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&sync[kSyncRouteDone], 1);
-    is_last = (prev == (int)gridDim.x - 1);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = blockIdx.x * kRouteWaves + threadIdx.x / kWave;
+  if (t < T) {
+    int sel[kTopK];
+    route_token(logits, bias, rsf, t, ids, w, sel);
+    if (lane < kTopK) {
+      int e = sel[0];
+#pragma unroll
+      for (int r = 1; r < kTopK; ++r)
+        if (lane == r) e = sel[r];
+      const int64_t le = (int64_t)e - offset;
+      if (le >= 0 && le < kELocal) atomicAdd(&hist[(int)le], 1);
+    }
+  }
+  __syncthreads();  // also makes this block's ids visible to all its threads
+  if (gridDim.x > 1) {
+    if (threadIdx.x < kELocal) block_hist[(size_t)blockIdx.x * kELocal + threadIdx.x] = hist[threadIdx.x];
+    return;
+  }
+  __shared__ PermShared sh;
+  if (threadIdx.x < kELocal) {
+    sh.total[threadIdx.x] = hist[threadIdx.x];
+    sh.before[threadIdx.x] = 0;
   }
   __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  build_permutation(ids, T, offset, pair_row, expert_off, perm_token);
-  if (threadIdx.x == 0) sync[kSyncRouteDone] = 0;  // reusable by the next call
+  if (threadIdx.x < kWave) expert_offsets(sh, true, expert_off);
+  __syncthreads();
+  scatter_chunk(ids, T, 0, offset, sh, pair_row, perm_token);
+}
+
+// Permutation for T > 16: workgroup c handles tokens [1024c, 1024c + 1024).
+// Every workgroup reduces the route histograms to the per-expert totals and to
+// the counts of the tokens before its chunk; workgroup 0 writes expert_off.
+__global__ void __launch_bounds__(kRouteThreads)
+perm_kernel(const int32_t* __restrict__ ids, int T, int64_t offset, const int32_t* __restrict__ block_hist,
+            int32_t* __restrict__ pair_row, int32_t* __restrict__ expert_off,
+            int32_t* __restrict__ perm_token) {
+  constexpr int kGroups = kRouteThreads / kELocal;                 // 32
+  constexpr int kRouteBlocksPerChunk = kRouteThreads / kRouteWaves;  // 64
+  __shared__ PermShared sh;
+  __shared__ int part_tot[kGroups][kELocal];
+  __shared__ int part_pre[kGroups][kELocal];
+  const int nb = (T + kRouteWaves - 1) / kRouteWaves;
+  const int first = blockIdx.x * kRouteBlocksPerChunk;
+  const int e = threadIdx.x % kELocal;
+  const int g = threadIdx.x / kELocal;
+  int tot = 0, pre = 0;
+  for (int b = g; b < nb; b += kGroups) {
+    const int v = block_hist[(size_t)b * kELocal + e];
+    tot += v;
+    if (b < first) pre += v;
+  }
+  part_tot[g][e] = tot;
+  part_pre[g][e] = pre;
+  __syncthreads();
+  if (threadIdx.x < kELocal) {
+    int a = 0, p = 0;
+#pragma unroll
+    for (int k = 0; k < kGroups; ++k) {
+      a += part_tot[k][threadIdx.x];
+      p += part_pre[k][threadIdx.x];
+    }
+    sh.total[threadIdx.x] = a;
+    sh.before[threadIdx.x] = p;
+  }
+  __syncthreads();
+  if (threadIdx.x < kWave) expert_offsets(sh, blockIdx.x == 0, expert_off);
+  __syncthreads();
+  scatter_chunk(ids, T, blockIdx.x * kRouteThreads, offset, sh, pair_row, perm_token);
 }
 
 }  // namespace
 
 hipError_t launch_route(const float* logits, const uint16_t* bias, float rsf, int T, int64_t offset,
                         const Layout& L, char* ws, hipStream_t stream) {
-  const int blocks = (T + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock;
-  hipLaunchKernelGGL(route_kernel, dim3(blocks), dim3(kRouteThreads), 0, stream, logits, bias, rsf,
-                     T, offset, (int32_t*)(ws + L.topk_ids), (float*)(ws + L.topk_w),
-                     (int32_t*)(ws + L.pair_row), (int32_t*)(ws + L.expert_off),
-                     (int32_t*)(ws + L.perm_token), (int32_t*)(ws + L.sync));
+  const int blocks = (T + kRouteWaves - 1) / kRouteWaves;
+  int32_t* ids = (int32_t*)(ws + L.topk_ids);
+  hipLaunchKernelGGL(route_kernel, dim3(blocks), dim3(kRouteThreads), 0, stream, logits, bias, rsf, T,
+                     offset, ids, (float*)(ws + L.topk_w), (int32_t*)(ws + L.pair_row),
+                     (int32_t*)(ws + L.expert_off), (int32_t*)(ws + L.perm_token),
+                     (int32_t*)(ws + L.block_hist));
+  if (blocks > 1) {
+    const int chunks = (T + kRouteThreads - 1) / kRouteThreads;
+    hipLaunchKernelGGL(perm_kernel, dim3(chunks), dim3(kRouteThreads), 0, stream, (const int32_t*)ids, T,
+                       offset, (const int32_t*)(ws + L.block_hist), (int32_t*)(ws + L.pair_row),
+                       (int32_t*)(ws + L.expert_off), (int32_t*)(ws + L.perm_token));
+  }
   return hipGetLastError();
 }
 

@@ -32,13 +32,13 @@ _ws: dict = {}
 
 
 def workspace(device: torch.device, T: int) -> torch.Tensor:
-    """Zero-initialised per-device workspace, grown on demand."""
+    """Per-device workspace, grown on demand (needs no initialisation)."""
     need = _lib.moe_lib().moe_fp8_ds_workspace_size(T)
     key = (device.type, device.index)
     with _ws_lock:
         buf = _ws.get(key)
         if buf is None or buf.numel() < need:
-            buf = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+            buf = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=device)
             _ws[key] = buf
         return buf
 
@@ -119,7 +119,7 @@ class RouteResult:
         self.perm_token = view(lay.perm_token, T * TOP_K, torch.int32)
         self.act = view(lay.act, T * TOP_K * I, torch.int16).view(T * TOP_K, I)
         self.down = view(lay.down, T * TOP_K * H, torch.int16).view(T * TOP_K, H)
-        self.sync = view(lay.sync, 64, torch.int32)
+        self.block_hist = view(lay.block_hist, (T + 15) // 16 * E_LOCAL, torch.int32).view(-1, E_LOCAL)
 
 
 def route(routing_logits, routing_bias, local_expert_offset, routed_scaling_factor, ws=None):

@@ -148,6 +148,20 @@ def test_layer_deterministic(pkg, cuda_device):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+def test_workspace_needs_no_initialisation(pkg, cuda_device):
+    """Garbage in the workspace does not change the result (no state is carried
+    between calls)."""
+    cfg = pkg.synth.CONFIGS["small_t64"]
+    w, _ = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, _ = gpu_tokens(pkg, cfg, cuda_device)
+    ws = pkg.workspace(cuda_device, 64)
+    outs = []
+    for fill in (0x00, 0xAB, 0xFF):
+        ws.fill_(fill)
+        outs.append(run_layer(pkg, tok, w, cfg.local_expert_offset, cfg.routed_scaling_factor).view(torch.int16))
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
 def test_synth_matches_cpu_generator(pkg, orc, cuda_device):
     """The GPU generator writes the same bytes as the oracle's CPU generator."""
     for name in ("plumbing_t16", "skewed_t8192"):

@@ -76,8 +76,10 @@ def test_route_matches_oracle(pkg, orc, cuda_device, name, offset, T):
                 assert offs[le] <= row < offs[le + 1] and perm[row] == t
             else:
                 assert pair[t, k] == -1
-    # the completion counter is left at zero for the next call
-    assert int(r.sync[0].item()) == 0
+    # per-workgroup histograms (T > 16 uses the two-kernel path) add up to the
+    # expert counts
+    if T > 16:
+        np.testing.assert_array_equal(r.block_hist.cpu().numpy().sum(axis=0), counts)
 
 
 def test_route_repeatable(pkg, cuda_device):
