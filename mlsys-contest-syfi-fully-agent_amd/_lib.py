@@ -18,7 +18,7 @@ OK, ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP, ERR_ARG = 0, -1, -2,
 
 class Layout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in
-                ("topk_ids", "topk_w", "pair_row", "expert_off", "perm_token", "act", "down", "block_hist", "total")]
+                ("topk_ids", "topk_w", "pair_row", "expert_off", "perm_token", "perm_w", "act", "down", "block_hist", "total")]
 
 
 _moe = None

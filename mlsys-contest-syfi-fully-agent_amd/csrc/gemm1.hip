@@ -6,158 +6,158 @@
 // G1[:, :I]); CUDA solution gemm_fp8_fp8_grouped_kernel (moe.cu:1373-1609) and
 // swiglu_kernel (moe.cu:2125-2146), which round-trip G1 through fp32 HBM.
 //
-// Design (gfx950):
-//   * v_mfma_f32_16x16x128_f8f6f4 covers exactly one 128-wide K scale block per
-//     instruction, so each MFMA yields the unscaled block partial P and the
-//     accumulator takes  acc += P * (a_scale[row, kb] * w_scale[n/128, kb]).
-//     fp8 x fp8 products are exact; only fp32 summation order differs from the
-//     fp32 reference.
-//   * each 16-column MFMA tile packs 8 gate columns (n0..n0+7) and the 8
-//     matching up columns (2048+n0..): the SwiGLU epilogue is one xor-8 lane
-//     shuffle, and a tile only needs 8 output columns, so even a single-token
-//     expert spreads over 256 workgroups (the HBM-bound decode case).
-//   * operands go straight from global memory into the MFMA register layout
-//     (both A and W13 are K-contiguous, so no transpose and no LDS staging);
-//     the token gather is fused into the A load (row -> perm_token -> hidden).
-//   * the 4 waves of a workgroup split the 56 K blocks; partials are summed
-//     through LDS before the epilogue.
+// Design (gfx950): v_mfma_f32_16x16x128_f8f6f4 covers exactly one 128-wide K
+// scale block per instruction, so each MFMA yields the unscaled block partial P
+// and the accumulator takes  acc += P * (a_scale[row, kb] * w_scale[n/128, kb]).
+// fp8 x fp8 products are exact; only the fp32 summation order differs from the
+// fp32 reference.  Gate column j and up column 2048 + j always land in the same
+// lane (or in lanes r and r + 8), so SwiGLU is fused into the epilogue and G1
+// never reaches HBM.  Two kernels:
+//   * streaming (small T): one workgroup per (expert, 8-column group), weights
+//     read once straight into registers -- HBM-bound;
+//   * tiled (large T): LDS-staged operand tiles, DMA pipeline -- MFMA-bound.
 #include "moe_common.hpp"
 
 namespace moe {
 namespace {
 
-constexpr int kG1Threads = 256;
-// Token count from which GEMM1 uses the LDS-tiled MFMA kernel.
-constexpr int kGemm1TiledMinTokens = 2048;
-constexpr int kG1Waves = kG1Threads / kWave;
+// ---------------------------------------------------------------------------
+// Streaming path (few rows per expert, T <= kGemm1StreamMaxTokens): bound by
+// reading the active experts' W13 once from HBM.
+//
+//   * a workgroup owns one (active expert, 8-column group): the 8 gate rows
+//     8c..8c+7 and the 8 matching up rows 2048+8c.. of W13 form one 16-column
+//     MFMA tile (lanes r < 8 gate, r >= 8 up), so even a single-token expert
+//     spreads over 256 workgroups and SwiGLU is one xor-8 lane exchange;
+//   * its 8 waves split K (7 scale blocks each) and issue all their weight
+//     loads before the first MFMA; every 16-row tile of the expert's tokens
+//     reuses them from registers;
+//   * kDirect (T <= 16): the MFMA rows are the T tokens themselves, so the
+//     activation loads need no permutation lookup and go out together with
+//     the weight loads; results are written to the permuted rows of the
+//     expert's tokens.  Otherwise the rows are the expert's permuted rows (the
+//     token gather is fused into the A load);
+//   * each wave copies its activation scales global -> LDS with
+//     global_load_lds_dword; the 8 K-partials are summed in LDS in a fixed
+//     order.
+// ---------------------------------------------------------------------------
+constexpr int kGemm1StreamMaxTokens = 64;
+constexpr int kGemm1DirectMaxTokens = 16;
+constexpr int kS1Waves = 8;
+constexpr int kS1Threads = kS1Waves * kWave;
+constexpr int kS1KB = kNHBlk / kS1Waves;  // 7 scale blocks per wave
+constexpr int kS1Groups = kI / 8;         // 256 column groups per expert
 
-template <int MI, int NJ>
-__global__ void __launch_bounds__(kG1Threads)
-gemm1_swiglu_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
+template <bool kDirect>
+__global__ void __launch_bounds__(kS1Threads)
+gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
                     const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                     const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
                     uint16_t* __restrict__ act) {
-  constexpr int BM = 16 * MI;
-  int e, row0, rows;
-  if (!find_row_tile(expert_off, blockIdx.y, BM, e, row0, rows)) return;
+  __shared__ float sa[kS1Waves][kS1KB][16];   // activation scales, per wave
+  __shared__ float red[kS1Waves][4][kWave];   // K-partials
+  __shared__ int inv[16];                     // kDirect: token -> permuted row, -1 if none
+  ExpertRows X;
+  X.load(expert_off);
+  const int cg = blockIdx.x % kS1Groups;
+  const int e = X.nth_active(blockIdx.x / kS1Groups);
+  if (e < 0) return;
+  const int row0 = X.begin(e);
+  const int M = X.end(e) - row0;
 
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x & (kWave - 1);
-  const int lr = lane & 15;  // operand row / output column inside a 16x16 tile
-  const int lq = lane >> 4;  // K quarter (operands) / output row group
+  const int lq = lane >> 4;
+  const int lr = lane & 15;
+  const int kb0 = wave * kS1KB;
+  const int n = lr < 8 ? 8 * cg + lr : kI + 8 * cg + (lr - 8);
+  // scale entries of this wave: entry x = (kb0 + x / 16, row x % 16), x < 112;
+  // lane l copies entries l and 64 + l
+  const int x1 = kWave + lane;
 
-  // A operand rows (gathered tokens); rows past the tile end repeat the last
-  // valid row so every load stays in bounds (their outputs are discarded).
-  const uint8_t* a_ptr[MI];
-  int out_tok[MI][4];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi) {
-    const int tok = perm_token[row0 + min(mi * 16 + lr, rows - 1)];
-    a_ptr[mi] = hs + (size_t)tok * kH + lq * 32;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out_tok[mi][i] = perm_token[row0 + min(mi * 16 + lq * 4 + i, rows - 1)];
-  }
-  // B operand rows: packed gate/up columns.
-  const uint8_t* b_ptr[NJ];
-  const float* bs_ptr[NJ];
-#pragma unroll
-  for (int nj = 0; nj < NJ; ++nj) {
-    const int n0 = (blockIdx.x * NJ + nj) * 8;
-    const int n = lr < 8 ? n0 + lr : kI + n0 + (lr - 8);
-    b_ptr[nj] = w13 + ((size_t)e * k2I + n) * kH + lq * 32;
-    bs_ptr[nj] = w13_scale + ((size_t)e * kN2IBlk + n / kBlk) * kNHBlk;
+  // kDirect: token of each permuted row of the expert (loaded now, used once
+  // all operand loads are in flight)
+  int my_tok = 0;
+  if (kDirect) {
+    if (threadIdx.x < 16) inv[threadIdx.x] = -1;
+    __syncthreads();
+    if (threadIdx.x < M) my_tok = perm_token[row0 + threadIdx.x];
   }
 
-  v4f acc[MI][NJ];
+  v8i b[kS1KB];
+  float sw[kS1KB];
+#pragma unroll 1
+  for (int rt = 0; rt * 16 < M; ++rt) {
+    const int rows = kDirect ? T : min(16, M - rt * 16);
+    int tok_a, tok_s0, tok_s1;
+    if (kDirect) {
+      tok_a = min(lr, rows - 1);
+      tok_s0 = min(lane & 15, rows - 1);
+      tok_s1 = min(x1 & 15, rows - 1);
+    } else {
+      const int* pt = perm_token + row0 + rt * 16;
+      tok_a = pt[min(lr, rows - 1)];
+      tok_s0 = pt[min(lane & 15, rows - 1)];
+      tok_s1 = pt[min(x1 & 15, rows - 1)];
+    }
+    dma4(hs_scale + (size_t)(kb0 + (lane >> 4)) * T + tok_s0, &sa[wave][0][0]);
+    if (x1 < kS1KB * 16) dma4(hs_scale + (size_t)(kb0 + (x1 >> 4)) * T + tok_s1, &sa[wave][4][0]);
+    if (rt == 0) {
+      const uint8_t* bp = w13 + ((size_t)e * k2I + n) * kH + kb0 * kBlk + 32 * lq;
 #pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
+      for (int j = 0; j < kS1KB; ++j) b[j] = *(const v8i*)(bp + j * kBlk);
+      const float* sp = w13_scale + ((size_t)e * kN2IBlk + n / kBlk) * kNHBlk + kb0;
 #pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
-
-#pragma unroll 2
-  for (int kb = wave; kb < kNHBlk; kb += kG1Waves) {
-    v8i a[MI], b[NJ];
+      for (int j = 0; j < kS1KB; ++j) sw[j] = sp[j];
+    }
+    v8i a[kS1KB];
+    const uint8_t* ap = hs + (size_t)tok_a * kH + kb0 * kBlk + 32 * lq;
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi) a[mi] = *(const v8i*)(a_ptr[mi] + kb * kBlk);
+    for (int j = 0; j < kS1KB; ++j) a[j] = *(const v8i*)(ap + j * kBlk);
+    // Every load of this wave, the scale DMA included, has landed before the
+    // first MFMA: the empty asm pins all operand registers here, so the
+    // compiler issues every load above it and cannot interleave loads with
+    // the MFMAs (which would serialise HBM round trips).
 #pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) b[nj] = *(const v8i*)(b_ptr[nj] + kb * kBlk);
-    float sa[MI][4], sw[NJ];
+    for (int j = 0; j < kS1KB; ++j) asm volatile("" : "+v"(a[j]), "+v"(b[j]));
+    wait_vmcnt_lgkm0<0>();
+    asm volatile("" ::: "memory");
+    if (kDirect && threadIdx.x < M) inv[my_tok] = row0 + threadIdx.x;  // read after the barrier below
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
+    for (int j = 0; j < kS1KB; ++j) {
+      const v4f p = mfma_f8_16x16x128(a[j], b[j]);
+      const v4f s = *(const v4f*)&sa[wave][j][4 * lq];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sa[mi][i] = hs_scale[(size_t)kb * T + out_tok[mi][i]];
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], s[i] * sw[j], acc[i]);
+    }
 #pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) sw[nj] = bs_ptr[nj][kb];
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int nj = 0; nj < NJ; ++nj) {
-        const v4f p = mfma_f8_16x16x128(a[mi], b[nj]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], sa[mi][i] * sw[nj], acc[mi][nj][i]);
-      }
-  }
-
-  // Sum the K-split partials of the 4 waves.
-  __shared__ float red[kG1Waves - 1][MI * NJ * 4][kWave];
-  if (wave > 0) {
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int nj = 0; nj < NJ; ++nj)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave - 1][(mi * NJ + nj) * 4 + i][lane] = acc[mi][nj][i];
-  }
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 0; w < kG1Waves - 1; ++w)
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int nj = 0; nj < NJ; ++nj)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mi][nj][i] += red[w][(mi * NJ + nj) * 4 + i][lane];
-
-  // SwiGLU (moe.py:190-193): lanes lr < 8 hold gate columns, lanes lr + 8 the
-  // matching up columns.
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) {
-      const int n0 = (blockIdx.x * NJ + nj) * 8;
+    for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
+    __syncthreads();
+    if (wave == 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float x1 = acc[mi][nj][i];
-        const float x2 = __shfl_xor(x1, 8, kWave);
-        const int r = mi * 16 + lq * 4 + i;
-        if (lr < 8 && r < rows) {
+        float v = red[0][i][lane];
+#pragma unroll
+        for (int w = 1; w < kS1Waves; ++w) v += red[w][i][lane];
+        // SwiGLU (moe.py:190-193): lanes r < 8 hold gate, lanes r + 8 the up column
+        const float x2 = __shfl_xor(v, 8, kWave);
+        const int r = 4 * lq + i;
+        const int prow = kDirect ? (r < rows ? inv[r] : -1) : (r < rows ? row0 + rt * 16 + r : -1);
+        if (lr < 8 && prow >= 0) {
           const float silu = x2 / (1.0f + expf(-x2));
-          act[(size_t)(row0 + r) * kI + n0 + lr] = f32_to_bf16_rne(silu * x1);
+          act[(size_t)prow * kI + 8 * cg + lr] = f32_to_bf16_rne(silu * v);
         }
       }
     }
+    if (kDirect) break;
+    __syncthreads();  // sa / red reused by the next row tile
+  }
 }
 
-// ---------------------------------------------------------------------------
-// Tiled path (many rows per expert): LDS-staged, MFMA-bound.
-//
-//   * workgroup = WM x WN waves; wave tile = (16*MI) rows x 64 MFMA columns,
-//     i.e. 32 gate columns j..j+31 and the 32 matching up columns 2048+j..;
-//     in the MFMA output layout a lane holds gate and up of the same (row,
-//     column), so SwiGLU needs no data movement;
-//   * one pipeline stage = one 128-wide K block (one scale block) of the A
-//     rows (gathered tokens), the B rows (W13), and the A scales;
-//   * stages are copied global -> LDS with global_load_lds_dwordx4 (no VGPR
-//     staging), 3 LDS buffers, loads for stage kb+2 in flight while stage kb
-//     is multiplied;
-//   * LDS holds each 16-row x 128-K operand fragment as two 1 KB planes in the
-//     MFMA register order (lane L = 16*q + r owns row r, K bytes 32q..32q+31),
-//     so every ds_read_b128 of the MFMA operands is contiguous across the wave
-//     (no bank conflicts) and every DMA writes one contiguous plane;
-//   * per K block: P = A_f8 * B_f8 (v_mfma_f32_16x16x128_f8f6f4, exact
-//     products), acc += P * (a_scale[row] * w_scale[n/128]).
-// ---------------------------------------------------------------------------
+// Token count from which GEMM1 uses 256-row tiles (below: 64-row tiles).
+constexpr int kGemm1TiledLargeMinTokens = 2048;
+
 template <int WM, int WN, int MI>
 struct G1Tiled {
   static constexpr int kWaves = WM * WN;
@@ -191,13 +191,15 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
   __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes];
 
   // ---- tile of this workgroup ------------------------------------------
-  const int mt_total = count_row_tiles(expert_off, C::BM);
+  ExpertRows X;
+  X.load(expert_off);
+  const int mt_total = X.count_tiles(C::BM);
   const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
   if (t < 0) return;
   int mt, nt;
   grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
   int e, row0, rows;
-  find_row_tile(expert_off, mt, C::BM, e, row0, rows);
+  X.find_tile(mt, C::BM, e, row0, rows);
   const int j0 = nt * C::kGateCols;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
@@ -325,31 +327,24 @@ hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, c
   return hipGetLastError();
 }
 
-template <int MI, int NJ>
-hipError_t launch_gemm1_cfg(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
-                            const float* w13_scale, const Layout& L, char* ws, int max_tiles,
-                            hipStream_t stream) {
-  const dim3 grid(kI / (8 * NJ), max_tiles);
-  hipLaunchKernelGGL((gemm1_swiglu_kernel<MI, NJ>), grid, dim3(kG1Threads), 0, stream, hs, hs_scale,
-                     T, w13, w13_scale, (const int32_t*)(ws + L.expert_off),
-                     (const int32_t*)(ws + L.perm_token), (uint16_t*)(ws + L.act));
-  return hipGetLastError();
-}
-
-// Upper bound on the number of row tiles of height bm over all experts.
-inline int max_row_tiles(int T, int bm) {
-  const int64_t pairs = (int64_t)T * kTopK;
-  const int64_t bound = (pairs + bm - 1) / bm + (pairs < kELocal ? pairs : kELocal);
-  return (int)(bound < pairs ? bound : pairs);
-}
-
 }  // namespace
 
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
                         const float* w13_scale, const Layout& L, char* ws, hipStream_t stream) {
-  if (T <= 8) return launch_gemm1_cfg<1, 1>(hs, hs_scale, T, w13, w13_scale, L, ws, max_row_tiles(T, 16), stream);
-  if (T < kGemm1TiledMinTokens)
-    return launch_gemm1_cfg<4, 4>(hs, hs_scale, T, w13, w13_scale, L, ws, max_row_tiles(T, 64), stream);
+  const int32_t* off = (const int32_t*)(ws + L.expert_off);
+  const int32_t* perm = (const int32_t*)(ws + L.perm_token);
+  uint16_t* act = (uint16_t*)(ws + L.act);
+  if (T <= kGemm1StreamMaxTokens) {
+    const int max_active = min(kELocal, T * kTopK);
+    if (T <= kGemm1DirectMaxTokens)
+      hipLaunchKernelGGL(gemm1_stream_kernel<true>, dim3(max_active * kS1Groups), dim3(kS1Threads), 0, stream,
+                         hs, hs_scale, T, w13, w13_scale, off, perm, act);
+    else
+      hipLaunchKernelGGL(gemm1_stream_kernel<false>, dim3(max_active * kS1Groups), dim3(kS1Threads), 0, stream,
+                         hs, hs_scale, T, w13, w13_scale, off, perm, act);
+    return hipGetLastError();
+  }
+  if (T < kGemm1TiledLargeMinTokens) return launch_gemm1_tiled<1, 4, 4>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
   return launch_gemm1_tiled<4, 2, 4>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
 }
 

@@ -11,121 +11,135 @@
 // e4m3 rounding of C (2^-4 relative) would break the 1e-2 tolerance; a hi/lo
 // e4m3 split costs the same MFMA time as bf16.
 //
-// Design: operands go straight from global memory into the MFMA layout (C rows
-// and W2 rows are both K-contiguous); the 4 waves split the 16 K blocks and
-// reduce through LDS; the fp32 rows are written for the combine pass.
-#include "moe_common.hpp"
+// Two kernels: a streaming one for small T (weights read once into
+// registers, the routing-weighted combine fused in) and an LDS-tiled one for
+// large T (MFMA-bound; rows go to the combine pass as bf16).
+#include "kernels.hpp"
 
 namespace moe {
 namespace {
 
-constexpr int kG2Threads = 256;
-// Token count from which GEMM2 uses the LDS-tiled MFMA kernel.
-constexpr int kGemm2TiledMinTokens = 2048;
-constexpr int kG2Waves = kG2Threads / kWave;
+// ---------------------------------------------------------------------------
+// Streaming path with the combine fused in (T <= kGemm2StreamMaxTokens).
+//
+//   * a workgroup owns 16 output columns n0..n0+15 for all T tokens; it walks
+//     the active experts in ascending order (the order of moe.py:168-200) and
+//     their 16-row tiles, computing O = act_rows . W2_e[n0..n0+15]^T;
+//   * its 8 waves split K (2 scale blocks each); the loads of the next
+//     (expert, row tile) job are issued before the current one is multiplied;
+//   * the K-partials are summed in LDS in a fixed order and each row's
+//     O * weight is added to its token's fp32 accumulator in LDS
+//     (acc = acc + O * w, the two roundings of moe.py:199-200); a token occurs
+//     at most once per expert, so no atomics are needed and the result is
+//     deterministic;
+//   * finally every token's 16 columns are rounded to bf16 and stored (tokens
+//     without a local expert get zeros).  No GEMM2 rows reach HBM and no
+//     separate combine pass runs.
+// ---------------------------------------------------------------------------
+constexpr int kS2Waves = 8;
+constexpr int kS2Threads = kS2Waves * kWave;
+constexpr int kS2KB = kNIBlk / kS2Waves;  // 2 scale blocks per wave
+constexpr int kS2Units = kH / 16;         // 448 column groups
 
-template <int MI, int NJ>
-__global__ void __launch_bounds__(kG2Threads)
-gemm2_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
-             const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
-             uint16_t* __restrict__ down) {
-  constexpr int BM = 16 * MI;
-  int e, row0, rows;
-  if (!find_row_tile(expert_off, blockIdx.y, BM, e, row0, rows)) return;
+struct S2Job {
+  int e, rt;  // expert, row tile; e < 0: none
+};
 
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int lr = lane & 15;
-  const int lq = lane >> 4;
-
-  const uint16_t* a_ptr[MI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi) a_ptr[mi] = act + (size_t)(row0 + min(mi * 16 + lr, rows - 1)) * kI + lq * 32;
-  const uint8_t* b_ptr[NJ];
-  const float* bs_ptr[NJ];
-#pragma unroll
-  for (int nj = 0; nj < NJ; ++nj) {
-    const int n = (blockIdx.x * NJ + nj) * 16 + lr;
-    b_ptr[nj] = w2 + ((size_t)e * kH + n) * kI + lq * 32;
-    bs_ptr[nj] = w2_scale + ((size_t)e * kNHBlk + n / kBlk) * kNIBlk;
-  }
-
-  v4f acc[MI][NJ];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
-
-#pragma unroll 2
-  for (int kb = wave; kb < kNIBlk; kb += kG2Waves) {
-    v8bf a[MI][4];
-    v8bf b[NJ][4];
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) a[mi][j] = *(const v8bf*)(a_ptr[mi] + kb * kBlk + j * 8);
-#pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) {
-      const v8i raw = *(const v8i*)(b_ptr[nj] + kb * kBlk);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[nj][j] = e4m3x8_to_bf16((uint32_t)raw[2 * j], (uint32_t)raw[2 * j + 1]);
-    }
-    float sw[NJ];
-#pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) sw[nj] = bs_ptr[nj][kb];
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int nj = 0; nj < NJ; ++nj) {
-        v4f p = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) p = mfma_bf16_16x16x32(a[mi][j], b[nj][j], p);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], sw[nj], acc[mi][nj][i]);
-      }
-  }
-
-  __shared__ float red[kG2Waves - 1][MI * NJ * 4][kWave];
-  if (wave > 0) {
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int nj = 0; nj < NJ; ++nj)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave - 1][(mi * NJ + nj) * 4 + i][lane] = acc[mi][nj][i];
-  }
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 0; w < kG2Waves - 1; ++w)
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int nj = 0; nj < NJ; ++nj)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mi][nj][i] += red[w][(mi * NJ + nj) * 4 + i][lane];
-
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) {
-      const int n = (blockIdx.x * NJ + nj) * 16 + lr;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = mi * 16 + lq * 4 + i;
-        if (r < rows) down[(size_t)(row0 + r) * kH + n] = f32_to_bf16_rne(acc[mi][nj][i]);
-      }
-    }
+// Next (expert, row tile) after `j` in ascending expert order (wave-level).
+__device__ __forceinline__ S2Job s2_next(const ExpertRows& X, uint32_t active, S2Job j) {
+  if (j.e >= 0 && (j.rt + 1) * 16 < X.end(j.e) - X.begin(j.e)) return {j.e, j.rt + 1};
+  const uint32_t later = j.e >= 0 ? active & ~((2u << j.e) - 1u) : active;
+  return later ? S2Job{__builtin_ctz(later), 0} : S2Job{-1, 0};
 }
 
-template <int MI, int NJ>
-hipError_t launch_gemm2_cfg(const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
-                            int max_tiles, hipStream_t stream) {
-  const dim3 grid(kH / (16 * NJ), max_tiles);
-  hipLaunchKernelGGL((gemm2_kernel<MI, NJ>), grid, dim3(kG2Threads), 0, stream,
-                     (const uint16_t*)(ws + L.act), w2, w2_scale,
-                     (const int32_t*)(ws + L.expert_off), (uint16_t*)(ws + L.down));
-  return hipGetLastError();
+struct S2Regs {
+  v8i b[kS2KB];      // e4m3 W2 rows, K = 32q .. 32q+31 of each scale block
+  v8i a[kS2KB][2];   // bf16 act rows, same K range
+  float sw[kS2KB];
+  int tok;           // token and weight of the row this thread combines
+  float pw;          //   (threads < 256: row = tid / 16 of the tile)
+};
+
+__device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
+                                        const int32_t* __restrict__ perm_token, const float* __restrict__ perm_w,
+                                        const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
+                                        const float* __restrict__ w2_scale, int n0, int kb0, int lq, int lr) {
+  const int row0 = X.begin(j.e) + j.rt * 16;
+  const int rows = min(16, X.end(j.e) - row0);
+  // combine operands first: waiting for them never waits for the prefetch
+  const int crow = row0 + min((int)(threadIdx.x >> 4) & 15, rows - 1);
+  R.tok = perm_token[crow];
+  R.pw = perm_w[crow];
+  const uint8_t* bp = w2 + ((size_t)j.e * kH + n0 + lr) * kI + kb0 * kBlk + 32 * lq;
+  const uint16_t* ap = act + (size_t)(row0 + min(lr, rows - 1)) * kI + kb0 * kBlk + 32 * lq;
+#pragma unroll
+  for (int k = 0; k < kS2KB; ++k) {
+    R.b[k] = *(const v8i*)(bp + k * kBlk);
+    R.a[k][0] = *(const v8i*)(ap + k * kBlk);
+    R.a[k][1] = *(const v8i*)(ap + k * kBlk + 16);
+    R.sw[k] = w2_scale[((size_t)j.e * kNHBlk + n0 / kBlk) * kNIBlk + kb0 + k];
+  }
+}
+
+__global__ void __launch_bounds__(kS2Threads)
+gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
+                     const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
+                     const int32_t* __restrict__ perm_token, const float* __restrict__ perm_w, int T,
+                     uint16_t* __restrict__ out) {
+  __shared__ float outacc[kGemm2StreamMaxTokens][16];
+  __shared__ float red[kS2Waves][256];
+  const int n0 = blockIdx.x * 16;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int lq = lane >> 4;
+  const int lr = lane & 15;
+  const int kb0 = wave * kS2KB;
+  for (int i = threadIdx.x; i < T * 16; i += kS2Threads) outacc[i >> 4][i & 15] = 0.f;
+
+  ExpertRows X;
+  X.load(expert_off);
+  const uint32_t active = X.active();
+  S2Job job = s2_next(X, active, {-1, 0});
+  S2Regs cur, nxt;
+  if (job.e >= 0) s2_load(cur, job, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
+  while (job.e >= 0) {
+    const S2Job nj = s2_next(X, active, job);
+    if (nj.e >= 0) s2_load(nxt, nj, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < kS2KB; ++k) {
+      v4f p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const v8i a = cur.a[k][h];
+        const v8bf a0 = __builtin_bit_cast(v8bf, v4i{a[0], a[1], a[2], a[3]});
+        const v8bf a1 = __builtin_bit_cast(v8bf, v4i{a[4], a[5], a[6], a[7]});
+        p = mfma_bf16_16x16x32(a0, e4m3x8_to_bf16((uint32_t)cur.b[k][4 * h], (uint32_t)cur.b[k][4 * h + 1]), p);
+        p = mfma_bf16_16x16x32(a1, e4m3x8_to_bf16((uint32_t)cur.b[k][4 * h + 2], (uint32_t)cur.b[k][4 * h + 3]), p);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], cur.sw[k], acc[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[wave][(4 * lq + i) * 16 + lr] = acc[i];
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      const int r = threadIdx.x >> 4, c = threadIdx.x & 15;
+      const int row = X.begin(job.e) + job.rt * 16 + r;
+      if (row < X.end(job.e)) {
+        float o = red[0][threadIdx.x];
+#pragma unroll
+        for (int w = 1; w < kS2Waves; ++w) o += red[w][threadIdx.x];
+        const float p = o * cur.pw;
+        outacc[cur.tok][c] = outacc[cur.tok][c] + p;
+      }
+    }
+    __syncthreads();
+    job = nj;
+    cur = nxt;
+  }
+  for (int i = threadIdx.x; i < T * 16; i += kS2Threads)
+    out[(size_t)(i >> 4) * kH + n0 + (i & 15)] = f32_to_bf16_rne(outacc[i >> 4][i & 15]);
 }
 
 // ---------------------------------------------------------------------------
@@ -144,6 +158,9 @@ hipError_t launch_gemm2_cfg(const uint8_t* w2, const float* w2_scale, const Layo
 //     with scale 1); P accumulates the two stages of a 128-K scale block on
 //     v_mfma_f32_16x16x32_bf16, then acc += P * w_scale[n/128, kb].
 // ---------------------------------------------------------------------------
+// Token count from which GEMM2 uses 128-row tiles (below: 64-row tiles).
+constexpr int kGemm2TiledLargeMinTokens = 2048;
+
 template <int WM, int WN, int MI, int NJ>
 struct G2Tiled {
   static constexpr int kWaves = WM * WN;
@@ -173,13 +190,15 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
   using C = G2Tiled<WM, WN, MI, NJ>;
   __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes];
 
-  const int mt_total = count_row_tiles(expert_off, C::BM);
+  ExpertRows X;
+  X.load(expert_off);
+  const int mt_total = X.count_tiles(C::BM);
   const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
   if (t < 0) return;
   int mt, nt;
   grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
   int e, row0, rows;
-  find_row_tile(expert_off, mt, C::BM, e, row0, rows);
+  X.find_tile(mt, C::BM, e, row0, rows);
   const int n0 = nt * C::BN;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -296,18 +315,19 @@ hipError_t launch_gemm2_tiled(int T, const uint8_t* w2, const float* w2_scale, c
   return hipGetLastError();
 }
 
-inline int max_row_tiles2(int T, int bm) {
-  const int64_t pairs = (int64_t)T * kTopK;
-  const int64_t bound = (pairs + bm - 1) / bm + (pairs < kELocal ? pairs : kELocal);
-  return (int)(bound < pairs ? bound : pairs);
-}
-
 }  // namespace
 
-hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
+bool gemm2_fuses_combine(int T) { return T <= kGemm2StreamMaxTokens; }
+
+hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws, void* out,
                         hipStream_t stream) {
-  if (T <= 8) return launch_gemm2_cfg<1, 1>(w2, w2_scale, L, ws, max_row_tiles2(T, 16), stream);
-  if (T < kGemm2TiledMinTokens) return launch_gemm2_cfg<4, 4>(w2, w2_scale, L, ws, max_row_tiles2(T, 64), stream);
+  if (gemm2_fuses_combine(T)) {
+    hipLaunchKernelGGL(gemm2_combine_kernel, dim3(kS2Units), dim3(kS2Threads), 0, stream,
+                       (const uint16_t*)(ws + L.act), w2, w2_scale, (const int32_t*)(ws + L.expert_off),
+                       (const int32_t*)(ws + L.perm_token), (const float*)(ws + L.perm_w), T, (uint16_t*)out);
+    return hipGetLastError();
+  }
+  if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<1, 4, 4, 4>(T, w2, w2_scale, L, ws, stream);
   return launch_gemm2_tiled<2, 4, 4, 4>(T, w2, w2_scale, L, ws, stream);
 }
 

@@ -9,7 +9,10 @@ hipError_t launch_route(const float* logits, const uint16_t* bias, float rsf, in
                         const Layout& L, char* ws, hipStream_t stream);
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
                         const float* w13_scale, const Layout& L, char* ws, hipStream_t stream);
-hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
+// Largest T for which GEMM2 also performs the weighted combine (no combine pass).
+constexpr int kGemm2StreamMaxTokens = 64;
+bool gemm2_fuses_combine(int T);
+hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws, void* out,
                         hipStream_t stream);
 hipError_t launch_combine(int T, const Layout& L, char* ws, void* out, hipStream_t stream);
 

@@ -59,6 +59,7 @@ int moe_fp8_ds_workspace_layout(int64_t T, moe_fp8_ds_layout* out) {
   out->pair_row = L.pair_row;
   out->expert_off = L.expert_off;
   out->perm_token = L.perm_token;
+  out->perm_w = L.perm_w;
   out->act = L.act;
   out->down = L.down;
   out->block_hist = L.block_hist;
@@ -114,9 +115,9 @@ static int run_layer(const float* routing_logits, const void* routing_bias, cons
                             (const uint8_t*)gemm1_weights, gemm1_weights_scale, L, ws, stream);
   mark(2);
   if (err == hipSuccess)
-    err = moe::launch_gemm2(t, (const uint8_t*)gemm2_weights, gemm2_weights_scale, L, ws, stream);
+    err = moe::launch_gemm2(t, (const uint8_t*)gemm2_weights, gemm2_weights_scale, L, ws, output, stream);
   mark(3);
-  if (err == hipSuccess) err = moe::launch_combine(t, L, ws, output, stream);
+  if (err == hipSuccess && !moe::gemm2_fuses_combine(t)) err = moe::launch_combine(t, L, ws, output, stream);
   mark(4);
   return err == hipSuccess ? MOE_FP8_DS_OK : MOE_FP8_DS_ERR_HIP;
 }

@@ -29,7 +29,7 @@ constexpr int kWave = 64;
 constexpr int64_t kMaxTokens = 1 << 20;
 
 struct Layout {
-  size_t topk_ids, topk_w, pair_row, expert_off, perm_token, act, down, block_hist, total;
+  size_t topk_ids, topk_w, pair_row, expert_off, perm_token, perm_w, act, down, block_hist, total;
 };
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -48,6 +48,7 @@ inline Layout make_layout(int64_t T) {
   L.topk_w = take(rows * sizeof(float));
   L.pair_row = take(rows * sizeof(int32_t));
   L.perm_token = take(rows * sizeof(int32_t));
+  L.perm_w = take(rows * sizeof(float));
   L.act = take(rows * kI * sizeof(uint16_t));
   L.down = take(rows * kH * sizeof(uint16_t));
   L.block_hist = take((size_t)((T + 15) / 16) * kELocal * sizeof(int32_t));
@@ -152,14 +153,6 @@ __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Number of row tiles of height bm over all local experts.
-__device__ __forceinline__ int count_row_tiles(const int32_t* __restrict__ off, int bm) {
-  int n = 0;
-#pragma unroll 1
-  for (int e = 0; e < kELocal; ++e) n += (off[e + 1] - off[e] + bm - 1) / bm;
-  return n;
-}
-
 // XCD-aware block -> tile map.  Workgroups are dispatched round-robin over the
 // 8 XCDs (block b runs on XCD b % 8), so block b takes tile
 //   (b % 8) * ceil(R / 8) + b / 8
@@ -184,25 +177,59 @@ __device__ __forceinline__ void grouped_tile(int t, int mt_total, int nt, int gm
   ntile = r / rows_in_group;
 }
 
-// Row m-tile lookup shared by the grouped GEMMs: global tile index `tile` ->
-// (local expert, first row, rows in tile) given the expert row offsets
-// off[0..32] and tile height bm.  Returns false past the last real tile.
-__device__ __forceinline__ bool find_row_tile(const int32_t* __restrict__ off, int tile, int bm,
-                                              int& expert, int& row0, int& rows) {
-  int acc = 0;
-#pragma unroll 1
-  for (int e = 0; e < kELocal; ++e) {
-    const int n = off[e + 1] - off[e];
-    const int tl = (n + bm - 1) / bm;
-    if (tile < acc + tl) {
-      expert = e;
-      row0 = off[e] + (tile - acc) * bm;
-      rows = min(bm, off[e + 1] - row0);
-      return true;
-    }
-    acc += tl;
+// The 33 expert row offsets spread over the lanes of a wave (lane x holds
+// off[x], lanes past 32 hold off[32]), read with one vector load.  Every query
+// is wave-level (ballot / readlane / lane scan): all 64 lanes of the wave must
+// call it, and the results are wave-uniform.
+struct ExpertRows {
+  int o;    // off[min(lane, 32)]
+  int cnt;  // rows of expert `lane` (lanes < 32), else 0
+
+  __device__ __forceinline__ void load(const int32_t* __restrict__ off) {
+    const int lane = threadIdx.x & (kWave - 1);
+    o = off[min(lane, kELocal)];
+    const int o1 = __shfl_down(o, 1, kWave);
+    cnt = lane < kELocal ? o1 - o : 0;
   }
-  return false;
-}
+  __device__ __forceinline__ int begin(int e) const { return __builtin_amdgcn_readlane(o, e); }
+  __device__ __forceinline__ int end(int e) const { return __builtin_amdgcn_readlane(o, e + 1); }
+  // Bit e set <=> expert e has rows.
+  __device__ __forceinline__ uint32_t active() const { return (uint32_t)__ballot(cnt > 0); }
+  // The slot-th expert with rows, or -1.
+  __device__ __forceinline__ int nth_active(int slot) const {
+    uint32_t m = active();
+    for (int k = 0; k < slot && m; ++k) m &= m - 1;
+    return m ? __builtin_ctz(m) : -1;
+  }
+  // Inclusive scan over experts of the number of row tiles of height bm.
+  __device__ __forceinline__ int tiles_incl(int bm) const {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nt = (cnt + bm - 1) / bm;
+    int incl = nt;
+#pragma unroll
+    for (int d = 1; d < kELocal; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += v;
+    }
+    return incl;
+  }
+  __device__ __forceinline__ int count_tiles(int bm) const {
+    return __builtin_amdgcn_readlane(tiles_incl(bm), kELocal - 1);
+  }
+  // Global row tile `tile` -> (expert, first row, rows in tile); false past the
+  // last tile.
+  __device__ __forceinline__ bool find_tile(int tile, int bm, int& e, int& row0, int& rows) const {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int incl = tiles_incl(bm);
+    const uint64_t m = __ballot(lane < kELocal && incl > tile);
+    if (!m) return false;
+    e = __builtin_ctzll(m);
+    const int nt = (cnt + bm - 1) / bm;
+    const int excl = __builtin_amdgcn_readlane(incl - nt, e);
+    row0 = begin(e) + (tile - excl) * bm;
+    rows = min(bm, end(e) - row0);
+    return true;
+  }
+};
 
 }  // namespace moe

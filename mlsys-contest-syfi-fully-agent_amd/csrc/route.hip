@@ -221,8 +221,9 @@ __device__ __forceinline__ void expert_offsets(PermShared& sh, bool write_off, i
 
 // Rows of the pairs of tokens [t0, t0 + 1024): ascending token order inside
 // each expert, starting at sh.running[e].  All 1024 threads take part.
-__device__ void scatter_chunk(const int32_t* __restrict__ ids, int T, int t0, int64_t offset, PermShared& sh,
-                              int32_t* __restrict__ pair_row, int32_t* __restrict__ perm_token) {
+__device__ void scatter_chunk(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int T, int t0,
+                              int64_t offset, PermShared& sh, int32_t* __restrict__ pair_row,
+                              int32_t* __restrict__ perm_token, float* __restrict__ perm_w) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -276,7 +277,10 @@ __device__ void scatter_chunk(const int32_t* __restrict__ ids, int T, int t0, in
     *(int4*)(pair_row + (size_t)t * kTopK + 4) = r1;
 #pragma unroll
     for (int k = 0; k < kTopK; ++k)
-      if (row[k] >= 0) perm_token[row[k]] = t;
+      if (row[k] >= 0) {
+        perm_token[row[k]] = t;
+        perm_w[row[k]] = topk_w[(size_t)t * kTopK + k];
+      }
   }
   __syncthreads();  // wave_cnt / wave_base may be reused
 }
@@ -288,7 +292,7 @@ __global__ void __launch_bounds__(kRouteThreads)
 route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf, int T,
              int64_t offset, int32_t* __restrict__ ids, float* __restrict__ w,
              int32_t* __restrict__ pair_row, int32_t* __restrict__ expert_off,
-             int32_t* __restrict__ perm_token, int32_t* __restrict__ block_hist) {
+             int32_t* __restrict__ perm_token, float* __restrict__ perm_w, int32_t* __restrict__ block_hist) {
   __shared__ int hist[kELocal];
   if (threadIdx.x < kELocal) hist[threadIdx.x] = 0;
   __syncthreads();
@@ -320,16 +324,16 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
   __syncthreads();
   if (threadIdx.x < kWave) expert_offsets(sh, true, expert_off);
   __syncthreads();
-  scatter_chunk(ids, T, 0, offset, sh, pair_row, perm_token);
+  scatter_chunk(ids, w, T, 0, offset, sh, pair_row, perm_token, perm_w);
 }
 
 // Permutation for T > 16: workgroup c handles tokens [1024c, 1024c + 1024).
 // Every workgroup reduces the route histograms to the per-expert totals and to
 // the counts of the tokens before its chunk; workgroup 0 writes expert_off.
 __global__ void __launch_bounds__(kRouteThreads)
-perm_kernel(const int32_t* __restrict__ ids, int T, int64_t offset, const int32_t* __restrict__ block_hist,
-            int32_t* __restrict__ pair_row, int32_t* __restrict__ expert_off,
-            int32_t* __restrict__ perm_token) {
+perm_kernel(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int T, int64_t offset,
+            const int32_t* __restrict__ block_hist, int32_t* __restrict__ pair_row,
+            int32_t* __restrict__ expert_off, int32_t* __restrict__ perm_token, float* __restrict__ perm_w) {
   constexpr int kGroups = kRouteThreads / kELocal;                 // 32
   constexpr int kRouteBlocksPerChunk = kRouteThreads / kRouteWaves;  // 64
   __shared__ PermShared sh;
@@ -361,7 +365,7 @@ perm_kernel(const int32_t* __restrict__ ids, int T, int64_t offset, const int32_
   __syncthreads();
   if (threadIdx.x < kWave) expert_offsets(sh, blockIdx.x == 0, expert_off);
   __syncthreads();
-  scatter_chunk(ids, T, blockIdx.x * kRouteThreads, offset, sh, pair_row, perm_token);
+  scatter_chunk(ids, topk_w, T, blockIdx.x * kRouteThreads, offset, sh, pair_row, perm_token, perm_w);
 }
 
 }  // namespace
@@ -373,12 +377,13 @@ hipError_t launch_route(const float* logits, const uint16_t* bias, float rsf, in
   hipLaunchKernelGGL(route_kernel, dim3(blocks), dim3(kRouteThreads), 0, stream, logits, bias, rsf, T,
                      offset, ids, (float*)(ws + L.topk_w), (int32_t*)(ws + L.pair_row),
                      (int32_t*)(ws + L.expert_off), (int32_t*)(ws + L.perm_token),
-                     (int32_t*)(ws + L.block_hist));
+                     (float*)(ws + L.perm_w), (int32_t*)(ws + L.block_hist));
   if (blocks > 1) {
     const int chunks = (T + kRouteThreads - 1) / kRouteThreads;
-    hipLaunchKernelGGL(perm_kernel, dim3(chunks), dim3(kRouteThreads), 0, stream, (const int32_t*)ids, T,
-                       offset, (const int32_t*)(ws + L.block_hist), (int32_t*)(ws + L.pair_row),
-                       (int32_t*)(ws + L.expert_off), (int32_t*)(ws + L.perm_token));
+    hipLaunchKernelGGL(perm_kernel, dim3(chunks), dim3(kRouteThreads), 0, stream, (const int32_t*)ids,
+                       (const float*)(ws + L.topk_w), T, offset, (const int32_t*)(ws + L.block_hist),
+                       (int32_t*)(ws + L.pair_row), (int32_t*)(ws + L.expert_off),
+                       (int32_t*)(ws + L.perm_token), (float*)(ws + L.perm_w));
   }
   return hipGetLastError();
 }

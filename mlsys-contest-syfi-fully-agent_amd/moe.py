@@ -26,6 +26,10 @@ import torch
 from . import _lib
 
 H, I, E_LOCAL, E_GLOBAL, TOP_K, BLOCK = 7168, 2048, 32, 256, 8, 128
+# Up to this T the GEMM2 kernel also performs the weighted combine and the
+# workspace's GEMM2 rows (`down`) are not written (kGemm2StreamMaxTokens in
+# csrc/kernels.hpp).
+FUSED_COMBINE_MAX_TOKENS = 64
 
 _ws_lock = threading.Lock()
 _ws: dict = {}
@@ -117,6 +121,7 @@ class RouteResult:
         self.pair_row = view(lay.pair_row, T * TOP_K, torch.int32).view(T, TOP_K)
         self.expert_off = view(lay.expert_off, E_LOCAL + 1, torch.int32)
         self.perm_token = view(lay.perm_token, T * TOP_K, torch.int32)
+        self.perm_w = view(lay.perm_w, T * TOP_K, torch.float32)
         self.act = view(lay.act, T * TOP_K * I, torch.int16).view(T * TOP_K, I)
         self.down = view(lay.down, T * TOP_K * H, torch.int16).view(T * TOP_K, H)
         self.block_hist = view(lay.block_hist, (T + 15) // 16 * E_LOCAL, torch.int32).view(-1, E_LOCAL)

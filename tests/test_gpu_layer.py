@@ -126,6 +126,8 @@ def test_intermediates_match_oracle(pkg, orc, cuda_device, name, T, n_rows):
     c_ref, o_ref = orc.expert_rows(x, perm[sel], le_all[sel])
     bad_c = bf16_close(act, c_ref, atol=1e-3, rtol=1e-2)
     assert not bad_c.any(), f"act: {int(bad_c.sum())} bad, rows {np.unique(np.nonzero(bad_c)[0])[:8]}"
+    if T <= pkg.moe.FUSED_COMBINE_MAX_TOKENS:
+        return  # GEMM2 rows are combined in registers, never stored
     bad_o = bf16_close(down, o_ref, atol=1e-2, rtol=1e-2)
     assert not bad_o.any(), f"down: {int(bad_o.sum())} bad, rows {np.unique(np.nonzero(bad_o)[0])[:8]}"
 

@@ -68,12 +68,14 @@ def test_route_matches_oracle(pkg, orc, cuda_device, name, offset, T):
     for le in range(32):
         np.testing.assert_array_equal(perm[offs[le]:offs[le + 1]], exp[le])
     pair = r.pair_row.cpu().numpy()
+    pw = r.perm_w.cpu().numpy()
     for t in range(T):
         for k in range(8):
             le = int(ids[t, k]) - off
             if 0 <= le < 32:
                 row = pair[t, k]
                 assert offs[le] <= row < offs[le + 1] and perm[row] == t
+                assert pw[row] == w[t, k]
             else:
                 assert pair[t, k] == -1
     # per-workgroup histograms (T > 16 uses the two-kernel path) add up to the
