@@ -103,6 +103,8 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     dma4(hs_scale + (size_t)(kb0 + (lane >> 4)) * T + tok_s0, &sa[wave][0][0]);
     if (x1 < kS1KB * 16) dma4(hs_scale + (size_t)(kb0 + (x1 >> 4)) * T + tok_s1, &sa[wave][4][0]);
     if (rt == 0) {
+      // this kernel's own K order: lane quarter q holds K bytes 32q .. 32q+31
+      // (measured faster than the 64-byte-run order for streaming from HBM)
       const uint8_t* bp = w13 + ((size_t)e * k2I + n) * kH + kb0 * kBlk + 32 * lq;
 #pragma unroll
       for (int j = 0; j < kS1KB; ++j) b[j] = *(const v8i*)(bp + j * kBlk);
@@ -146,7 +148,7 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
         const int prow = kDirect ? (r < rows ? inv[r] : -1) : (r < rows ? row0 + rt * 16 + r : -1);
         if (lr < 8 && prow >= 0) {
           const float silu = x2 / (1.0f + expf(-x2));
-          act[(size_t)prow * kI + 8 * cg + lr] = f32_to_bf16_rne(silu * v);
+          act[(size_t)prow * kI + act_store_col(8 * cg + lr)] = f32_to_bf16_rne(silu * v);
         }
       }
     }
@@ -155,6 +157,26 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tiled path (many rows per expert): LDS-staged, MFMA-bound.
+//
+//   * workgroup = WM x WN waves; wave tile = (16*MI) rows x 64 MFMA columns,
+//     i.e. 32 gate columns j..j+31 and the 32 matching up columns 2048+j..;
+//     in the MFMA output layout a lane holds gate and up of the same (row,
+//     column), so SwiGLU needs no data movement;
+//   * one pipeline stage = one 128-wide K block (one scale block) of the A
+//     rows (gathered tokens), the B rows (W13), and the A scales;
+//   * stages are copied global -> LDS with global_load_lds_dwordx4 (no VGPR
+//     staging) into a ring of kStages LDS buffers, the loads of stage
+//     kb + kStages - 1 in flight while stage kb is multiplied;
+//   * LDS holds each 16-row x 128-K operand fragment as two 1 KB planes in
+//     MFMA register order (lane L = 16q + r owns row r, K bytes 16q.. of plane
+//     0 and 64+16q.. of plane 1), so every ds_read_b128 of the MFMA operands is
+//     contiguous across the wave (no bank conflicts) and every DMA reads 64
+//     contiguous bytes of each of 16 rows;
+//   * per K block: P = A_f8 * B_f8 (v_mfma_f32_16x16x128_f8f6f4, exact
+//     products), acc += P * (a_scale[row] * w_scale[n/128]).
+// ---------------------------------------------------------------------------
 // Token count from which GEMM1 uses 256-row tiles (below: 64-row tiles).
 constexpr int kGemm1TiledLargeMinTokens = 2048;
 
@@ -171,7 +193,9 @@ struct G1Tiled {
   static constexpr int kBOff = kAFrags * kFrag;
   static constexpr int kSOff = kBOff + kBFrags * kFrag;
   static constexpr int kStageBytes = kSOff + BM * 4;
+  static constexpr int kWscBytes = WN * 2 * kNHBlk * 4;  // weight block scales (after the stages)
   static constexpr int kStages = 3;
+  static_assert(kStages >= 2 && kStages <= 4, "pipeline depth");
   static constexpr int kPlanes = 2 * (kAFrags + kBFrags);
   static_assert(kPlanes % kWaves == 0, "planes must split evenly over waves");
   static constexpr int kPlanesPerWave = kPlanes / kWaves;
@@ -188,7 +212,10 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
                    const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
                    uint16_t* __restrict__ act) {
   using C = G1Tiled<WM, WN, MI>;
-  __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes];
+  // One LDS object: the stage ring, then the weight scale table.  (A second
+  // __shared__ array makes the compiler wait for every outstanding LDS DMA
+  // before any LDS read, which would serialise the pipeline.)
+  __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
 
   // ---- tile of this workgroup ------------------------------------------
   ExpertRows X;
@@ -216,7 +243,7 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
   for (int k = 0; k < C::kPlanesPerWave; ++k) {
     const int plane = wave + k * C::kWaves;
     const int frag = plane >> 1, half = plane & 1;
-    const int kofs = 32 * lq + 16 * half;
+    const int kofs = 16 * lq + 64 * half;  // K order of the e4m3 operands
     if (frag < C::kAFrags) {
       const int r = min(frag * 16 + lr, rows - 1);
       src[k] = hs + (size_t)perm_token[row0 + r] * kH + kofs;
@@ -240,9 +267,14 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
     if (sload) dma4(ssrc + (size_t)kb * T, base + sdst);
   };
 
-  // weight block scales of this wave's gate / up columns
-  const float* sg_ptr = w13_scale + ((size_t)e * kN2IBlk + (j0 + 32 * wn) / kBlk) * kNHBlk;
-  const float* su_ptr = w13_scale + ((size_t)e * kN2IBlk + (kI + j0 + 32 * wn) / kBlk) * kNHBlk;
+  // Weight block scales of every wave's gate / up columns, staged in LDS once
+  // (no scalar loads in the main loop: they would force full lgkmcnt waits).
+  float* wsc = (float*)(lds + C::kStages * C::kStageBytes);  // [WN][2][56]
+  for (int i = threadIdx.x; i < WN * 2 * kNHBlk; i += C::kThreads) {
+    const int w_n = i / (2 * kNHBlk), up = (i / kNHBlk) & 1, kb = i % kNHBlk;
+    const int blk = (up ? kI : 0) + j0 + 32 * w_n;
+    wsc[i] = w13_scale[((size_t)e * kN2IBlk + blk / kBlk) * kNHBlk + kb];
+  }
 
   v4f acc[MI][4];
 #pragma unroll
@@ -250,52 +282,51 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  issue(0);
-  issue(1);
+#pragma unroll
+  for (int s = 0; s < C::kStages - 1; ++s) issue(s);
 #pragma unroll 1
   for (int kb = 0; kb < kNHBlk; ++kb) {
-    if (kb + 1 < kNHBlk)
-      wait_vmcnt_lgkm0<C::kDmaPerStage>();
-    else
-      wait_vmcnt_lgkm0<0>();
+    // stages kb+1 .. kb+kStages-2 may stay in flight
+    wait_stages_ahead<C::kDmaPerStage>(min(kNHBlk - 1 - kb, C::kStages - 2));
     block_barrier();
-    if (kb + 2 < kNHBlk) issue(kb + 2);
+    if (kb + C::kStages - 1 < kNHBlk) issue(kb + C::kStages - 1);
 
     const char* sb = lds + (kb % C::kStages) * C::kStageBytes;
-    v8i a[MI], b[4];
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-      const char* f = sb + (wm * MI + mi) * C::kFrag + lane * 16;
+    // B fragments and the first A fragment first; the reads of A fragment
+    // mi + 1 and of row scales overlap the MFMAs of fragment mi.
+    auto read_frag = [&](int off) {
+      const char* f = sb + off + lane * 16;
       const v4i lo = *(const v4i*)f, hi = *(const v4i*)(f + 1024);
-      a[mi] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
+      return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    v8i b[4];
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
       const int bf = nj < 2 ? 2 * wn + nj : 2 * WN + 2 * wn + (nj - 2);
-      const char* f = sb + C::kBOff + bf * C::kFrag + lane * 16;
-      const v4i lo = *(const v4i*)f, hi = *(const v4i*)(f + 1024);
-      b[nj] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      b[nj] = read_frag(C::kBOff + bf * C::kFrag);
     }
-    const float sg = sg_ptr[kb], su = su_ptr[kb];
-    v4f sgm[MI], sum[MI];
+    const float sg = wsc[(2 * wn) * kNHBlk + kb], su = wsc[(2 * wn + 1) * kNHBlk + kb];
+    v8i a_cur = read_frag((wm * MI) * C::kFrag);
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
+      v8i a_nxt;
+      if (mi + 1 < MI) a_nxt = read_frag((wm * MI + mi + 1) * C::kFrag);
       const v4f sa = *(const v4f*)(sb + C::kSOff + (wm * 16 * MI + 16 * mi + 4 * lq) * 4);
+      v4f sgm, sum;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sgm[mi][i] = sa[i] * sg;
-        sum[mi][i] = sa[i] * su;
+        sgm[i] = sa[i] * sg;
+        sum[i] = sa[i] * su;
       }
-    }
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int nj = 0; nj < 4; ++nj) {
-        const v4f p = mfma_f8_16x16x128(a[mi], b[nj]);
-        const v4f s = nj < 2 ? sgm[mi] : sum[mi];
+        const v4f p = mfma_f8_16x16x128(a_cur, b[nj]);
+        const v4f sc = nj < 2 ? sgm : sum;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], s[i], acc[mi][nj][i]);
+        for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], sc[i], acc[mi][nj][i]);
       }
+      if (mi + 1 < MI) a_cur = a_nxt;
+    }
   }
 
   // ---- SwiGLU epilogue (moe.py:190-193): act = silu(up) * gate ------------
@@ -309,7 +340,7 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
         if (r < rows) {
           const float x1 = acc[mi][nj][i], x2 = acc[mi][nj + 2][i];
           const float silu = x2 / (1.0f + expf(-x2));
-          act[(size_t)(row0 + r) * kI + j0 + 32 * wn + 16 * nj + lr] = f32_to_bf16_rne(silu * x1);
+          act[(size_t)(row0 + r) * kI + act_store_col(j0 + 32 * wn + 16 * nj + lr)] = f32_to_bf16_rne(silu * x1);
         }
       }
 }

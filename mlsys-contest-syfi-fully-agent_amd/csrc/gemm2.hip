@@ -53,8 +53,8 @@ __device__ __forceinline__ S2Job s2_next(const ExpertRows& X, uint32_t active, S
 }
 
 struct S2Regs {
-  v8i b[kS2KB];      // e4m3 W2 rows, K = 32q .. 32q+31 of each scale block
-  v8i a[kS2KB][2];   // bf16 act rows, same K range
+  v4i b[kS2KB][2];     // e4m3 W2 row bytes 64g + 16q .. +15 of each scale block
+  v4i a[kS2KB][2][2];  // bf16 act (stored order): elements 64g + 32h + 8q .. +7
   float sw[kS2KB];
   int tok;           // token and weight of the row this thread combines
   float pw;          //   (threads < 256: row = tid / 16 of the tile)
@@ -70,13 +70,16 @@ __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
   const int crow = row0 + min((int)(threadIdx.x >> 4) & 15, rows - 1);
   R.tok = perm_token[crow];
   R.pw = perm_w[crow];
-  const uint8_t* bp = w2 + ((size_t)j.e * kH + n0 + lr) * kI + kb0 * kBlk + 32 * lq;
-  const uint16_t* ap = act + (size_t)(row0 + min(lr, rows - 1)) * kI + kb0 * kBlk + 32 * lq;
+  const uint8_t* bp = w2 + ((size_t)j.e * kH + n0 + lr) * kI + kb0 * kBlk + 16 * lq;
+  const uint16_t* ap = act + (size_t)(row0 + min(lr, rows - 1)) * kI + kb0 * kBlk + 8 * lq;
 #pragma unroll
   for (int k = 0; k < kS2KB; ++k) {
-    R.b[k] = *(const v8i*)(bp + k * kBlk);
-    R.a[k][0] = *(const v8i*)(ap + k * kBlk);
-    R.a[k][1] = *(const v8i*)(ap + k * kBlk + 16);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      R.b[k][g] = *(const v4i*)(bp + k * kBlk + 64 * g);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) R.a[k][g][h] = *(const v4i*)(ap + k * kBlk + 64 * g + 32 * h);
+    }
     R.sw[k] = w2_scale[((size_t)j.e * kNHBlk + n0 / kBlk) * kNIBlk + kb0 + k];
   }
 }
@@ -110,12 +113,12 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
     for (int k = 0; k < kS2KB; ++k) {
       v4f p = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const v8i a = cur.a[k][h];
-        const v8bf a0 = __builtin_bit_cast(v8bf, v4i{a[0], a[1], a[2], a[3]});
-        const v8bf a1 = __builtin_bit_cast(v8bf, v4i{a[4], a[5], a[6], a[7]});
-        p = mfma_bf16_16x16x32(a0, e4m3x8_to_bf16((uint32_t)cur.b[k][4 * h], (uint32_t)cur.b[k][4 * h + 1]), p);
-        p = mfma_bf16_16x16x32(a1, e4m3x8_to_bf16((uint32_t)cur.b[k][4 * h + 2], (uint32_t)cur.b[k][4 * h + 3]), p);
+      for (int g = 0; g < 2; ++g) {
+        const v4i b = cur.b[k][g];
+        p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][0]),
+                               e4m3x8_to_bf16((uint32_t)b[0], (uint32_t)b[1]), p);
+        p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][1]),
+                               e4m3x8_to_bf16((uint32_t)b[2], (uint32_t)b[3]), p);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], cur.sw[k], acc[i]);
@@ -152,8 +155,8 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
 //   * operand fragments sit in LDS in MFMA register order: an A fragment
 //     (16 rows x 64 K bf16) is two 1 KB planes, a B fragment (16 rows x 64 K
 //     e4m3) one plane; lane L = 16*q + r owns row r, K = 16q .. 16q+15 of the
-//     stage (instruction j of the stage takes K = 16q + 8j .. +7 -- the same
-//     K permutation for A and B, so the dot products are unchanged);
+//     stage, instruction j taking K = 16q + 8j .. +7 (the act columns are
+//     stored so that these are 16 contiguous bytes: act_store_col);
 //   * B is widened e4m3 -> bf16 exactly in registers (v_cvt_scalef32_pk_bf16_fp8
 //     with scale 1); P accumulates the two stages of a 128-K scale block on
 //     v_mfma_f32_16x16x32_bf16, then acc += P * w_scale[n/128, kb].
@@ -174,7 +177,9 @@ struct G2Tiled {
   static constexpr int kBFrags = BN / 16;
   static constexpr int kBOff = kAFrags * 2048;
   static constexpr int kStageBytes = kBOff + kBFrags * 1024;
+  static constexpr int kWscBytes = WN * kNIBlk * 4;  // weight block scales (after the stages)
   static constexpr int kStages = 4;
+  static_assert(kStages >= 2 && kStages <= 5, "pipeline depth");
   static constexpr int kSteps = kI / 64;  // stages per tile (two per scale block)
   static constexpr int kPlanes = 2 * kAFrags + kBFrags;
   static_assert(kPlanes % kWaves == 0, "planes must split evenly over waves");
@@ -188,7 +193,8 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
                    const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
                    uint16_t* __restrict__ down) {
   using C = G2Tiled<WM, WN, MI, NJ>;
-  __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes];
+  // One LDS object (see gemm1.hip): the stage ring, then the weight scales.
+  __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
 
   ExpertRows X;
   X.load(expert_off);
@@ -217,7 +223,7 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
     if (plane < 2 * C::kAFrags) {
       const int f = plane >> 1, p = plane & 1;
       const int r = min(f * 16 + lr, rows - 1);
-      src[k] = (const char*)(act + (size_t)(row0 + r) * kI + 16 * lq + 8 * p);
+      src[k] = (const char*)(act + (size_t)(row0 + r) * kI + 32 * p + 8 * lq);  // stored order
       dst[k] = f * 2048 + p * 1024;
     } else {
       const int f = plane - 2 * C::kAFrags;
@@ -233,7 +239,12 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
       dma16(src[k] + step, base + dst[k]);
     }
   };
-  const float* sb_ptr = w2_scale + ((size_t)e * kNHBlk + (n0 + 16 * NJ * wn) / kBlk) * kNIBlk;
+  // weight block scales of every wave's columns, staged in LDS once
+  float* wsc = (float*)(lds + C::kStages * C::kStageBytes);  // [WN][16]
+  for (int i = threadIdx.x; i < WN * kNIBlk; i += C::kThreads) {
+    const int w_n = i / kNIBlk, kb = i % kNIBlk;
+    wsc[i] = w2_scale[((size_t)e * kNHBlk + (n0 + 16 * NJ * w_n) / kBlk) * kNIBlk + kb];
+  }
 
   v4f acc[MI][NJ], P[MI][NJ];
 #pragma unroll
@@ -246,13 +257,7 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
 #pragma unroll 1
   for (int s = 0; s < C::kSteps; ++s) {
     // stages s+1 .. s+kStages-2 may stay in flight
-    const int ahead = min(C::kSteps - 1 - s, C::kStages - 2);
-    if (ahead >= 2)
-      wait_vmcnt_lgkm0<2 * C::kPlanesPerWave>();
-    else if (ahead == 1)
-      wait_vmcnt_lgkm0<C::kPlanesPerWave>();
-    else
-      wait_vmcnt_lgkm0<0>();
+    wait_stages_ahead<C::kPlanesPerWave>(min(C::kSteps - 1 - s, C::kStages - 2));
     block_barrier();
     if (s + C::kStages - 1 < C::kSteps) issue(s + C::kStages - 1);
 
@@ -278,7 +283,7 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
         P[mi][nj] = mfma_bf16_16x16x32(a[mi][1], b[nj][1], P[mi][nj]);
       }
     if (s & 1) {
-      const float sb = sb_ptr[s >> 1];
+      const float sb = wsc[wn * kNIBlk + (s >> 1)];
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll

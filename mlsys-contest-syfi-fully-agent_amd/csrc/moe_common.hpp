@@ -57,6 +57,25 @@ inline Layout make_layout(int64_t T) {
 }
 
 // ---------------------------------------------------------------------------
+// Operand K order.  An MFMA sums over K, so any permutation of K that A and B
+// share leaves each dot product unchanged; the kernels pick the one that
+// makes every 16-byte load part of a 64-byte contiguous run per row (a 32-byte
+// stride between the pieces of a row costs ~3x in L2 -> LDS throughput).
+//   * e4m3 operands of the tiled GEMM1 (16x16x128 MFMA): the lane at quarter
+//     q (lanes 16q..16q+15) holds K bytes 16q..16q+15 and 64+16q..64+16q+15
+//     of the 128-K block (the streaming GEMM1 keeps 32q..32q+31: its weights
+//     stream from HBM, where that order measured faster);
+//   * bf16 activation rows (`act`, written by GEMM1, read by GEMM2): inside
+//     each group of 64 columns, logical column 16q + 8h + i (q < 4, h < 2,
+//     i < 8) is stored at 32h + 8q + i, so the 16 bytes stored at 32h + 8q ..
+//     (one contiguous load) are the K indices that pair with the h-th half of
+//     the 16 weight bytes a GEMM2 lane loads at 16q.
+// ---------------------------------------------------------------------------
+__host__ __device__ constexpr int act_store_col(int c) {
+  return (c & ~63) + 32 * ((c >> 3) & 1) + 8 * ((c >> 4) & 3) + (c & 7);
+}
+
+// ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -144,6 +163,20 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt_lgkm0() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+}
+
+// Waits until at most `ahead` pipeline stages of `per_stage` vector-memory
+// operations each are still in flight (ahead = 0, 1, 2, 3).
+template <int per_stage>
+__device__ __forceinline__ void wait_stages_ahead(int ahead) {
+  if (ahead >= 3)
+    wait_vmcnt_lgkm0<3 * per_stage>();
+  else if (ahead == 2)
+    wait_vmcnt_lgkm0<2 * per_stage>();
+  else if (ahead == 1)
+    wait_vmcnt_lgkm0<per_stage>();
+  else
+    wait_vmcnt_lgkm0<0>();
 }
 
 // Workgroup barrier that the compiler may not move memory accesses across.
