@@ -171,6 +171,23 @@ def measure(pkg, torch, wl, iters, trials, warmup):
     }
 
 
+def measured_traffic(workload, stage):
+    """HBM bytes per launch of `stage` on `workload` from the committed rocprofv3
+    counter summaries (profiles/*.txt lines 'TRAFFIC stage=S workload=W
+    fetch_bytes=F write_bytes=B', already scaled by the copy calibration), or
+    None when no summary covers it."""
+    import glob
+
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.txt"))):
+        for line in open(path):
+            if not line.startswith("TRAFFIC "):
+                continue
+            kv = dict(tok.split("=", 1) for tok in line.split()[1:] if "=" in tok)
+            if kv.get("stage") == stage and kv.get("workload") == workload:
+                return int(kv["fetch_bytes"]) + int(kv["write_bytes"])
+    return None
+
+
 def copy_calibration(torch, dev, mib):
     """A plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE
     counters of a --pmc run of this script."""
@@ -236,7 +253,7 @@ def main():
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--trials", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-tokens", type=int, default=64)
+    ap.add_argument("--cpu-tokens", type=int, default=1024)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this size (for PMC byte calibration)")
     args = ap.parse_args()
@@ -274,7 +291,8 @@ def main():
 
     dom = hm["dominant"]
     roof = {"bound": dom["bound"], "achieved": round(dom["achieved"], 3), "peak": dom["peak"],
-            "unit": dom["unit"], "frac": round(dom["frac"], 4), "traffic": None,
+            "unit": dom["unit"], "frac": round(dom["frac"], 4),
+            "traffic": measured_traffic(args.workload, dom["kernel"]),
             "kernel": dom["kernel"], "kernel_us": round(dom["ms"] * 1e3, 3)}
     cpu = None if args.no_cpu else cpu_baseline(pkg, torch, head, args.cpu_tokens)
 
