@@ -84,36 +84,23 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     if (threadIdx.x < M) my_tok = perm_token[row0 + threadIdx.x];
   }
 
+  // Token index of this lane's A row for row tile rt (kDirect: the token is
+  // the row itself).  Lanes of one row share it; so do the scale entries a
+  // lane copies (entries l and 64 + l both have row l % 16).
+  auto tile_token = [&](int rt) {
+    const int rows = kDirect ? T : min(16, M - rt * 16);
+    return kDirect ? min(lr, rows - 1) : perm_token[row0 + rt * 16 + min(lr, rows - 1)];
+  };
+
   v8i b[kS1KB];
   float sw[kS1KB];
-#pragma unroll 1
-  for (int rt = 0; rt * 16 < M; ++rt) {
+  // One 16-row tile: scale DMA, A loads, MFMAs, K reduction, SwiGLU, store.
+  auto row_tile = [&](int rt, int tok) {
     const int rows = kDirect ? T : min(16, M - rt * 16);
-    int tok_a, tok_s0, tok_s1;
-    if (kDirect) {
-      tok_a = min(lr, rows - 1);
-      tok_s0 = min(lane & 15, rows - 1);
-      tok_s1 = min(x1 & 15, rows - 1);
-    } else {
-      const int* pt = perm_token + row0 + rt * 16;
-      tok_a = pt[min(lr, rows - 1)];
-      tok_s0 = pt[min(lane & 15, rows - 1)];
-      tok_s1 = pt[min(x1 & 15, rows - 1)];
-    }
-    dma4(hs_scale + (size_t)(kb0 + (lane >> 4)) * T + tok_s0, &sa[wave][0][0]);
-    if (x1 < kS1KB * 16) dma4(hs_scale + (size_t)(kb0 + (x1 >> 4)) * T + tok_s1, &sa[wave][4][0]);
-    if (rt == 0) {
-      // this kernel's own K order: lane quarter q holds K bytes 32q .. 32q+31
-      // (measured faster than the 64-byte-run order for streaming from HBM)
-      const uint8_t* bp = w13 + ((size_t)e * k2I + n) * kH + kb0 * kBlk + 32 * lq;
-#pragma unroll
-      for (int j = 0; j < kS1KB; ++j) b[j] = *(const v8i*)(bp + j * kBlk);
-      const float* sp = w13_scale + ((size_t)e * kN2IBlk + n / kBlk) * kNHBlk + kb0;
-#pragma unroll
-      for (int j = 0; j < kS1KB; ++j) sw[j] = sp[j];
-    }
+    dma4(hs_scale + (size_t)(kb0 + (lane >> 4)) * T + tok, &sa[wave][0][0]);
+    if (x1 < kS1KB * 16) dma4(hs_scale + (size_t)(kb0 + (x1 >> 4)) * T + tok, &sa[wave][4][0]);
     v8i a[kS1KB];
-    const uint8_t* ap = hs + (size_t)tok_a * kH + kb0 * kBlk + 32 * lq;
+    const uint8_t* ap = hs + (size_t)tok * kH + kb0 * kBlk + 32 * lq;
 #pragma unroll
     for (int j = 0; j < kS1KB; ++j) a[j] = *(const v8i*)(ap + j * kBlk);
     // Every load of this wave, the scale DMA included, has landed before the
@@ -129,9 +116,9 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
 #pragma unroll
     for (int j = 0; j < kS1KB; ++j) {
       const v4f p = mfma_f8_16x16x128(a[j], b[j]);
-      const v4f s = *(const v4f*)&sa[wave][j][4 * lq];
+      const v4f sc = *(const v4f*)&sa[wave][j][4 * lq];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], s[i] * sw[j], acc[i]);
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], sc[i] * sw[j], acc[i]);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
@@ -152,8 +139,30 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
         }
       }
     }
-    if (kDirect) break;
-    __syncthreads();  // sa / red reused by the next row tile
+  };
+
+  // Row tile 0 in straight-line code: its token index load goes out first and
+  // the weight loads right after it, so waiting for the index (in-order vmcnt)
+  // leaves every weight load in flight.
+  const int tok0 = tile_token(0);
+  {
+    // this kernel's own K order: lane quarter q holds K bytes 32q .. 32q+31
+    // (measured faster than the 64-byte-run order for streaming from HBM)
+    const uint8_t* bp = w13 + ((size_t)e * k2I + n) * kH + kb0 * kBlk + 32 * lq;
+#pragma unroll
+    for (int j = 0; j < kS1KB; ++j) b[j] = *(const v8i*)(bp + j * kBlk);
+    const float* sp = w13_scale + ((size_t)e * kN2IBlk + n / kBlk) * kNHBlk + kb0;
+#pragma unroll
+    for (int j = 0; j < kS1KB; ++j) sw[j] = sp[j];
+  }
+  row_tile(0, tok0);
+  if (!kDirect) {
+#pragma unroll 1
+    for (int rt = 1; rt * 16 < M; ++rt) {
+      const int tok = tile_token(rt);
+      __syncthreads();  // sa / red of the previous tile consumed
+      row_tile(rt, tok);
+    }
   }
 }
 
