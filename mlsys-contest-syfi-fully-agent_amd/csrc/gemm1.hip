@@ -201,15 +201,19 @@ struct G1Tiled {
   static constexpr int kFrag = 2048;            // bytes of a 16 x 128 fp8 fragment
   static constexpr int kBOff = kAFrags * kFrag;
   static constexpr int kSOff = kBOff + kBFrags * kFrag;
-  static constexpr int kStageBytes = kSOff + BM * 4;
+  // Activation scales: every lane of every wave DMAs one dword (a branch on
+  // the lane would split the main loop into basic blocks and keep the MFMA
+  // results live across them), so each wave owns a 64-dword slot whose first
+  // kScaleRowsPerWave entries are its rows' scales.
+  static constexpr int kStageBytes = kSOff + kWaves * kWave * 4;
   static constexpr int kWscBytes = WN * 2 * kNHBlk * 4;  // weight block scales (after the stages)
   static constexpr int kStages = 3;
-  static_assert(kStages >= 2 && kStages <= 4, "pipeline depth");
+  static_assert(kStages >= 2 && kStages <= 4, "pipeline depth (wait_stages_ahead)");
   static constexpr int kPlanes = 2 * (kAFrags + kBFrags);
   static_assert(kPlanes % kWaves == 0, "planes must split evenly over waves");
   static constexpr int kPlanesPerWave = kPlanes / kWaves;
   static constexpr int kScaleRowsPerWave = BM / kWaves;
-  static_assert(kScaleRowsPerWave >= 1 && kScaleRowsPerWave <= kWave, "scale rows per wave");
+  static_assert(kScaleRowsPerWave % 4 == 0 && kScaleRowsPerWave <= kWave, "scale rows per wave");
   static constexpr int kDmaPerStage = kPlanesPerWave + 1;
   static constexpr int kGroupM = 4;             // row tiles per L2 group
 };
@@ -266,14 +270,13 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
   }
   const int srow = wave * C::kScaleRowsPerWave + lane;
   const float* ssrc = hs_scale + perm_token[row0 + min(srow, rows - 1)];
-  const bool sload = lane < C::kScaleRowsPerWave;
-  const int sdst = C::kSOff + wave * C::kScaleRowsPerWave * 4;
+  const int sdst = C::kSOff + wave * kWave * 4;
 
   auto issue = [&](int kb) {
     char* base = lds + (kb % C::kStages) * C::kStageBytes;
 #pragma unroll
     for (int k = 0; k < C::kPlanesPerWave; ++k) dma16(src[k] + kb * kBlk, base + dst[k]);
-    if (sload) dma4(ssrc + (size_t)kb * T, base + sdst);
+    dma4(ssrc + (size_t)kb * T, base + sdst);
   };
 
   // Weight block scales of every wave's gate / up columns, staged in LDS once
@@ -291,52 +294,99 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
 
+  // Software pipeline.  At iteration kb the operands of stage kb are already
+  // in registers (read during iteration kb - 1), so
+  //   * its LDS buffer takes the DMA of stage kb + kStages at once (the DMA
+  //     stays kStages - 1 stages ahead of the LDS reads), and
+  //   * the LDS reads of stage kb + 1 overlap the MFMAs of stage kb.
+  struct Frags {
+    v8i a[MI], b[4];
+    v4f sa[MI];
+    float sg, su;
+  };
+  auto frag = [&](int s, int off) {
+    const char* f = lds + (s % C::kStages) * C::kStageBytes + off + lane * 16;
+    const v4i lo = *(const v4i*)f, hi = *(const v4i*)(f + 1024);
+    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+  auto read_b = [&](int s, Frags& F) {
 #pragma unroll
-  for (int s = 0; s < C::kStages - 1; ++s) issue(s);
-#pragma unroll 1
-  for (int kb = 0; kb < kNHBlk; ++kb) {
-    // stages kb+1 .. kb+kStages-2 may stay in flight
-    wait_stages_ahead<C::kDmaPerStage>(min(kNHBlk - 1 - kb, C::kStages - 2));
-    block_barrier();
-    if (kb + C::kStages - 1 < kNHBlk) issue(kb + C::kStages - 1);
-
-    const char* sb = lds + (kb % C::kStages) * C::kStageBytes;
-    // B fragments and the first A fragment first; the reads of A fragment
-    // mi + 1 and of row scales overlap the MFMAs of fragment mi.
-    auto read_frag = [&](int off) {
-      const char* f = sb + off + lane * 16;
-      const v4i lo = *(const v4i*)f, hi = *(const v4i*)(f + 1024);
-      return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    };
-    v8i b[4];
+    for (int nj = 0; nj < 4; ++nj) F.b[nj] = frag(s, C::kBOff + (nj < 2 ? 2 * wn + nj : 2 * WN + 2 * wn + (nj - 2)) * C::kFrag);
+    F.sg = wsc[(2 * wn) * kNHBlk + s];
+    F.su = wsc[(2 * wn + 1) * kNHBlk + s];
+  };
+  auto read_a = [&](int s, int mi, Frags& F) {
+    F.a[mi] = frag(s, (wm * MI + mi) * C::kFrag);
+    const int r = wm * 16 * MI + 16 * mi + 4 * lq;  // 4 rows in one wave's slot
+    const int slot = (r / C::kScaleRowsPerWave) * kWave + r % C::kScaleRowsPerWave;
+    F.sa[mi] = *(const v4f*)(lds + (s % C::kStages) * C::kStageBytes + C::kSOff + slot * 4);
+  };
+  auto compute_row = [&](const Frags& F, int mi) {
+    v4f sgm, sum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sgm[i] = F.sa[mi][i] * F.sg;
+      sum[i] = F.sa[mi][i] * F.su;
+    }
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
-      const int bf = nj < 2 ? 2 * wn + nj : 2 * WN + 2 * wn + (nj - 2);
-      b[nj] = read_frag(C::kBOff + bf * C::kFrag);
+      const v4f p = mfma_f8_16x16x128(F.a[mi], F.b[nj]);
+      const v4f sc = nj < 2 ? sgm : sum;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], sc[i], acc[mi][nj][i]);
     }
-    const float sg = wsc[(2 * wn) * kNHBlk + kb], su = wsc[(2 * wn + 1) * kNHBlk + kb];
-    v8i a_cur = read_frag((wm * MI) * C::kFrag);
+  };
+  auto compute = [&](const Frags& F) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) compute_row(F, mi);
+  };
+
+  // One pipeline step: stage kb+1 has landed (later stages may stay in
+  // flight) and this wave's reads of stage kb are complete (the wait also
+  // drains LDS reads), so after the barrier stage kb's buffer is free.
+  // The A fragment of row block mi of stage kb+1 is read once the MFMAs of
+  // row block mi of stage kb have taken theirs, so both stages' A fragments
+  // are never live at once.
+  auto step = [&](int kb, const Frags& c, Frags& n, int ahead, bool refill) {
+    wait_stages_ahead<C::kDmaPerStage>(ahead);
+    block_barrier();
+    if (refill) issue(kb + C::kStages);
+    read_b(kb + 1, n);
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      v8i a_nxt;
-      if (mi + 1 < MI) a_nxt = read_frag((wm * MI + mi + 1) * C::kFrag);
-      const v4f sa = *(const v4f*)(sb + C::kSOff + (wm * 16 * MI + 16 * mi + 4 * lq) * 4);
-      v4f sgm, sum;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sgm[i] = sa[i] * sg;
-        sum[i] = sa[i] * su;
-      }
-#pragma unroll
-      for (int nj = 0; nj < 4; ++nj) {
-        const v4f p = mfma_f8_16x16x128(a_cur, b[nj]);
-        const v4f sc = nj < 2 ? sgm : sum;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], sc[i], acc[mi][nj][i]);
-      }
-      if (mi + 1 < MI) a_cur = a_nxt;
+      compute_row(c, mi);
+      __builtin_amdgcn_sched_barrier(0);
+      read_a(kb + 1, mi, n);
     }
+  };
+  // Two fragment sets used alternately (no register copies between steps);
+  // every branch below is resolved at compile time, so the compiler sees
+  // straight-line code between the explicit waits.
+  constexpr int kRefill = kNHBlk - C::kStages;  // steps that refill their buffer
+  constexpr int kPairs = kRefill / 2;
+  Frags f0, f1;
+#pragma unroll
+  for (int s = 0; s < C::kStages; ++s) issue(s);
+  wait_stages_ahead<C::kDmaPerStage>(C::kStages - 1);  // stage 0 landed
+  block_barrier();
+  read_b(0, f0);
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) read_a(0, mi, f0);
+#pragma unroll 1
+  for (int p = 0; p < kPairs; ++p) {
+    step(2 * p, f0, f1, C::kStages - 2, true);
+    step(2 * p + 1, f1, f0, C::kStages - 2, true);
   }
+#pragma unroll
+  for (int kb = 2 * kPairs; kb < kNHBlk - 1; ++kb) {
+    const bool refill = kb < kRefill;
+    const int ahead = min(C::kStages - 2, kNHBlk - 2 - kb);
+    if (kb & 1)
+      step(kb, f1, f0, ahead, refill);
+    else
+      step(kb, f0, f1, ahead, refill);
+  }
+  compute(((kNHBlk - 1) & 1) ? f1 : f0);
 
   // ---- SwiGLU epilogue (moe.py:190-193): act = silu(up) * gate ------------
 #pragma unroll
@@ -367,6 +417,204 @@ hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, c
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Wide path (large T): 256 rows x 256 MFMA columns per workgroup.
+//
+// With 256 x 128 tiles the kernel is bound by the L2 -> LDS feed, not by the
+// MFMAs: each CU sustains only a fixed number of outstanding L2 lines, so its
+// copy rate is capped near (lines in flight x 128 B) / L2 latency.  A 256 x 256
+// tile moves (256 + 256) x 128 B per K block for 2 x 256 x 256 x 128 FLOP, a
+// third less per FLOP than 256 x 128.
+//
+//   * 8 waves as 4 (rows) x 2 (columns); wave tile = 64 rows x (64 gate + the
+//     64 matching up columns), 4 x 8 MFMA blocks, 128 accumulator VGPRs;
+//   * the workgroup's 128 gate columns (and its 128 up columns) are one
+//     128-column weight scale block, so one gate and one up scale per K block;
+//   * two LDS stages of 66 KB: the copy of K block kb + 1 runs while K block
+//     kb is multiplied;
+//   * the DMA sources are a wave-uniform base plus a 32-bit lane offset
+//     (saddr form), one VGPR per copied plane.
+// ---------------------------------------------------------------------------
+struct G1Wide {
+  static constexpr int kWaves = 8;
+  static constexpr int kThreads = kWave * kWaves;
+  static constexpr int WM = 4, WN = 2;
+  static constexpr int MI = 4;                   // 16-row blocks per wave
+  static constexpr int NJ = 4;                   // 16-column gate blocks per wave (and as many up)
+  static constexpr int BM = 16 * MI * WM;        // 256 rows
+  static constexpr int kGateCols = 16 * NJ * WN; // 128 act columns
+  static constexpr int kNT = kI / kGateCols;     // 16 column tiles
+  static constexpr int kAFrags = BM / 16;        // 16
+  static constexpr int kBFrags = 2 * kGateCols / 16;  // 16: 8 gate + 8 up
+  static constexpr int kFrag = 2048;
+  static constexpr int kBOff = kAFrags * kFrag;
+  static constexpr int kSOff = kBOff + kBFrags * kFrag;
+  static constexpr int kStageBytes = kSOff + kWaves * kWave * 4;  // + one 64-dword scale slot per wave
+  static constexpr int kStages = 2;
+  static constexpr int kWscBytes = 2 * kNHBlk * 4;
+  static constexpr int kPlanes = 2 * (kAFrags + kBFrags);
+  static constexpr int kPlanesPerWave = kPlanes / kWaves;       // 8: 4 A + 4 B
+  static constexpr int kScaleRowsPerWave = BM / kWaves;         // 32
+  static constexpr int kGroupM = 4;
+  static_assert(kGateCols == kBlk, "one weight scale block per tile");
+  static_assert(kPlanes % kWaves == 0 && (kAFrags * 2) % kWaves == 0, "planes split evenly");
+  static_assert(kScaleRowsPerWave % 4 == 0 && kScaleRowsPerWave <= kWave, "scale rows per wave");
+  static_assert(kStages * kStageBytes + kWscBytes <= 160 * 1024, "LDS");
+};
+
+__global__ void __launch_bounds__(G1Wide::kThreads)
+gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
+                  const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
+                  const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
+                  uint16_t* __restrict__ act) {
+  using C = G1Wide;
+  __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
+
+  ExpertRows X;
+  X.load(expert_off);
+  const int mt_total = X.count_tiles(C::BM);
+  const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
+  if (t < 0) return;
+  int mt, nt;
+  grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
+  int e, row0, rows;
+  X.find_tile(mt, C::BM, e, row0, rows);
+  const int j0 = nt * C::kGateCols;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int lq = lane >> 4;
+  const int lr = lane & 15;
+  const int wm = wave / C::WN;
+  const int wn = wave % C::WN;
+
+  // ---- DMA planes of this wave: planes wave + 8k; k < 4 are A, k >= 4 are B
+  const uint8_t* w13e = w13 + (size_t)e * k2I * kH;
+  uint32_t off[C::kPlanesPerWave];
+  int dst[C::kPlanesPerWave];
+#pragma unroll
+  for (int k = 0; k < C::kPlanesPerWave; ++k) {
+    const int plane = wave + k * C::kWaves;
+    const int frag = plane >> 1, half = plane & 1;
+    const uint32_t kofs = 16 * lq + 64 * half;  // K order of the e4m3 operands
+    if (frag < C::kAFrags) {
+      const int r = min(frag * 16 + lr, rows - 1);
+      off[k] = (uint32_t)perm_token[row0 + r] * kH + kofs;
+      dst[k] = frag * C::kFrag + half * 1024;
+    } else {
+      const int bf = frag - C::kAFrags;  // 0..7 gate, 8..15 up
+      const int n = bf < 8 ? j0 + 16 * bf + lr : kI + j0 + 16 * (bf - 8) + lr;
+      off[k] = (uint32_t)n * kH + kofs;
+      dst[k] = C::kBOff + bf * C::kFrag + half * 1024;
+    }
+  }
+  const uint32_t stok = (uint32_t)perm_token[row0 + min(wave * C::kScaleRowsPerWave + lane, rows - 1)];
+  const int sdst = C::kSOff + wave * kWave * 4;
+
+  auto issue = [&](int kb) {
+    char* base = lds + (kb & 1) * C::kStageBytes;
+    const uint8_t* hk = hs + kb * kBlk;
+    const uint8_t* wk = w13e + kb * kBlk;
+#pragma unroll
+    for (int k = 0; k < C::kPlanesPerWave; ++k) dma16((k < C::kPlanesPerWave / 2 ? hk : wk) + off[k], base + dst[k]);
+    dma4(hs_scale + (size_t)kb * T + stok, base + sdst);
+  };
+
+  // weight block scales of the tile's gate block and up block, per K block
+  float* wsc = (float*)(lds + C::kStages * C::kStageBytes);  // [2][56]
+  for (int i = threadIdx.x; i < 2 * kNHBlk; i += C::kThreads) {
+    const int up = i / kNHBlk, kb = i % kNHBlk;
+    wsc[i] = w13_scale[((size_t)e * kN2IBlk + (up ? kI : 0) / kBlk + j0 / kBlk) * kNHBlk + kb];
+  }
+
+  v4f acc[C::MI][2 * C::NJ];
+#pragma unroll
+  for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < 2 * C::NJ; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int kb) {
+    const char* sb = lds + (kb & 1) * C::kStageBytes;
+    auto frag = [&](int off_) {
+      const char* f = sb + off_ + lane * 16;
+      const v4i lo = *(const v4i*)f, hi = *(const v4i*)(f + 1024);
+      return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    };
+    v8i b[2 * C::NJ];
+#pragma unroll
+    for (int nj = 0; nj < C::NJ; ++nj) {
+      b[nj] = frag(C::kBOff + (C::NJ * wn + nj) * C::kFrag);                  // gate
+      b[C::NJ + nj] = frag(C::kBOff + (8 + C::NJ * wn + nj) * C::kFrag);      // up
+    }
+    const float sg = wsc[kb], su = wsc[kNHBlk + kb];
+#pragma unroll
+    for (int mi = 0; mi < C::MI; ++mi) {
+      const v8i a = frag((C::MI * wm + mi) * C::kFrag);
+      const int r = C::MI * 16 * wm + 16 * mi + 4 * lq;  // 4 rows in one wave's scale slot
+      const int slot = (r / C::kScaleRowsPerWave) * kWave + r % C::kScaleRowsPerWave;
+      const v4f sa = *(const v4f*)(sb + C::kSOff + slot * 4);
+      v4f sgm, sum;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sgm[i] = sa[i] * sg;
+        sum[i] = sa[i] * su;
+      }
+#pragma unroll
+      for (int nj = 0; nj < 2 * C::NJ; ++nj) {
+        const v4f p = mfma_f8_16x16x128(a, b[nj]);
+        const v4f sc = nj < C::NJ ? sgm : sum;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], sc[i], acc[mi][nj][i]);
+      }
+      // keep each row block's MFMA results short-lived (otherwise the
+      // scheduler hoists all 32 MFMAs and runs out of registers)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Step kb: stage kb has landed (the only copy in flight) and every wave has
+  // finished reading stage kb - 1, so after the barrier that buffer takes the
+  // copy of stage kb + 1 while stage kb is multiplied.
+  issue(0);
+#pragma unroll 1
+  for (int kb = 0; kb < kNHBlk - 1; ++kb) {
+    wait_vmcnt_lgkm0<0>();
+    block_barrier();
+    issue(kb + 1);
+    compute(kb);
+  }
+  wait_vmcnt_lgkm0<0>();
+  block_barrier();
+  compute(kNHBlk - 1);
+
+  // ---- SwiGLU epilogue (moe.py:190-193): act = silu(up) * gate ------------
+#pragma unroll
+  for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < C::NJ; ++nj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = C::MI * 16 * wm + 16 * mi + 4 * lq + i;
+        if (r < rows) {
+          const float x1 = acc[mi][nj][i], x2 = acc[mi][C::NJ + nj][i];
+          const float silu = x2 / (1.0f + expf(-x2));
+          act[(size_t)(row0 + r) * kI + act_store_col(j0 + 16 * (C::NJ * wn + nj) + lr)] = f32_to_bf16_rne(silu * x1);
+        }
+      }
+}
+
+hipError_t launch_gemm1_wide(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
+                             const float* w13_scale, const Layout& L, char* ws, hipStream_t stream) {
+  using C = G1Wide;
+  const int64_t pairs = (int64_t)T * kTopK;
+  const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
+  const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
+  hipLaunchKernelGGL(gemm1_wide_kernel, dim3((unsigned)blocks), dim3(C::kThreads), 0, stream, hs, hs_scale, T,
+                     w13, w13_scale, (const int32_t*)(ws + L.expert_off), (const int32_t*)(ws + L.perm_token),
+                     (uint16_t*)(ws + L.act));
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
@@ -385,7 +633,7 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const u
     return hipGetLastError();
   }
   if (T < kGemm1TiledLargeMinTokens) return launch_gemm1_tiled<1, 4, 4>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
-  return launch_gemm1_tiled<4, 2, 4>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
+  return launch_gemm1_wide(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
 }
 
 }  // namespace moe
