@@ -516,7 +516,11 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
     const uint8_t* hk = hs + kb * kBlk;
     const uint8_t* wk = w13e + kb * kBlk;
 #pragma unroll
-    for (int k = 0; k < C::kPlanesPerWave; ++k) dma16((k < C::kPlanesPerWave / 2 ? hk : wk) + off[k], base + dst[k]);
+    for (int k = 0; k < C::kPlanesPerWave; ++k) {
+      const bool a_plane = k < C::kPlanesPerWave / 2;
+      // A fragments wholly past the tile's rows are never read: no copy
+      if (!a_plane || ((wave + k * C::kWaves) >> 1) * 16 < rows) dma16((a_plane ? hk : wk) + off[k], base + dst[k]);
+    }
     dma4(hs_scale + (size_t)kb * T + stok, base + sdst);
   };
 
@@ -572,6 +576,10 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
     }
   };
 
+  // Waves whose 64 rows all lie past the tile's rows (small experts) only
+  // help with the copies.
+  const bool wave_live = C::MI * 16 * wm < rows;
+
   // Step kb: stage kb has landed (the only copy in flight) and every wave has
   // finished reading stage kb - 1, so after the barrier that buffer takes the
   // copy of stage kb + 1 while stage kb is multiplied.
@@ -581,11 +589,11 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
     wait_vmcnt_lgkm0<0>();
     block_barrier();
     issue(kb + 1);
-    compute(kb);
+    if (wave_live) compute(kb);
   }
   wait_vmcnt_lgkm0<0>();
   block_barrier();
-  compute(kNHBlk - 1);
+  if (wave_live) compute(kNHBlk - 1);
 
   // ---- SwiGLU epilogue (moe.py:190-193): act = silu(up) * gate ------------
 #pragma unroll

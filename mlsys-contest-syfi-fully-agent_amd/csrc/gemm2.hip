@@ -320,6 +320,189 @@ hipError_t launch_gemm2_tiled(int T, const uint8_t* w2, const float* w2_scale, c
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Wide path (large T): 256 rows x 256 columns per workgroup, for the same
+// reason as GEMM1's wide path -- the L2 -> LDS copy rate per CU, not the
+// MFMAs, bounds the 128 x 256 tiles, and a 256 x 256 tile copies 48 KB instead
+// of 64 KB per 8.4 MFLOP.
+//
+//   * 8 waves as 4 (rows) x 2 (columns); wave tile 64 rows x 128 columns (one
+//     128-column weight scale block), 4 x 8 MFMA blocks, 128 accumulator VGPRs;
+//   * the scale is applied per 64-K stage (acc += P_stage * w_scale[n/128,
+//     k/128]), so no second set of block partials stays live across stages;
+//   * three 48 KB LDS stages, the copies of stages s+1 and s+2 in flight while
+//     stage s is multiplied; operand layouts as in the tiled path.
+// ---------------------------------------------------------------------------
+struct G2Wide {
+  static constexpr int kWaves = 8;
+  static constexpr int kThreads = kWave * kWaves;
+  static constexpr int WM = 4, WN = 2, MI = 4, NJ = 8;
+  static constexpr int BM = 16 * MI * WM;  // 256
+  static constexpr int BN = 16 * NJ * WN;  // 256
+  static constexpr int kNT = kH / BN;      // 28
+  static_assert(kH % BN == 0 && 16 * NJ == kBlk, "a wave's columns are one scale block");
+  static constexpr int kAFrags = BM / 16;
+  static constexpr int kBFrags = BN / 16;
+  static constexpr int kBOff = kAFrags * 2048;
+  static constexpr int kStageBytes = kBOff + kBFrags * 1024;  // 48 KB
+  static constexpr int kStages = 3;
+  static constexpr int kWscBytes = WN * kNIBlk * 4;
+  static constexpr int kSteps = kI / 64;
+  static constexpr int kPlanes = 2 * kAFrags + kBFrags;
+  static constexpr int kPlanesPerWave = kPlanes / kWaves;  // 6: 4 A + 2 B
+  static constexpr int kGroupM = 4;
+  static_assert(kPlanes % kWaves == 0 && (2 * kAFrags) % kWaves == 0, "planes split evenly");
+  static_assert(kStages * kStageBytes + kWscBytes <= 160 * 1024, "LDS");
+};
+
+__global__ void __launch_bounds__(G2Wide::kThreads)
+gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
+                  const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
+                  uint16_t* __restrict__ down) {
+  using C = G2Wide;
+  __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
+
+  ExpertRows X;
+  X.load(expert_off);
+  const int mt_total = X.count_tiles(C::BM);
+  const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
+  if (t < 0) return;
+  int mt, nt;
+  grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
+  int e, row0, rows;
+  X.find_tile(mt, C::BM, e, row0, rows);
+  const int n0 = nt * C::BN;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int lq = lane >> 4;
+  const int lr = lane & 15;
+  const int wm = wave / C::WN;
+  const int wn = wave % C::WN;
+
+  // DMA planes wave + 8k: k < 4 are A planes (bf16 act rows), k >= 4 B planes
+  const char* actb = (const char*)(act + (size_t)row0 * kI);
+  const uint8_t* w2e = w2 + (size_t)e * kH * kI;
+  uint32_t off[C::kPlanesPerWave];
+  int dst[C::kPlanesPerWave];
+#pragma unroll
+  for (int k = 0; k < C::kPlanesPerWave; ++k) {
+    const int plane = wave + k * C::kWaves;
+    if (plane < 2 * C::kAFrags) {
+      const int f = plane >> 1, p = plane & 1;
+      const int r = min(f * 16 + lr, rows - 1);
+      off[k] = (uint32_t)(r * kI + 32 * p + 8 * lq) * 2;  // stored order
+      dst[k] = f * 2048 + p * 1024;
+    } else {
+      const int f = plane - 2 * C::kAFrags;
+      off[k] = (uint32_t)(n0 + 16 * f + lr) * kI + 16 * lq;
+      dst[k] = C::kBOff + f * 1024;
+    }
+  }
+  auto issue = [&](int s) {
+    char* base = lds + (s % C::kStages) * C::kStageBytes;
+    const char* ak = actb + s * 64 * 2;
+    const uint8_t* wk = w2e + s * 64;
+#pragma unroll
+    for (int k = 0; k < C::kPlanesPerWave; ++k) {
+      const bool a_plane = k < 2 * C::kAFrags / C::kWaves;
+      // A fragments wholly past the tile's rows are never read: no copy
+      if (a_plane) {
+        if (((wave + k * C::kWaves) >> 1) * 16 < rows) dma16(ak + off[k], base + dst[k]);
+      } else {
+        dma16(wk + off[k], base + dst[k]);
+      }
+    }
+  };
+  float* wsc = (float*)(lds + C::kStages * C::kStageBytes);  // [WN][16]
+  for (int i = threadIdx.x; i < C::WN * kNIBlk; i += C::kThreads) {
+    const int w_n = i / kNIBlk, kb = i % kNIBlk;
+    wsc[i] = w2_scale[((size_t)e * kNHBlk + (n0 + 16 * C::NJ * w_n) / kBlk) * kNIBlk + kb];
+  }
+
+  v4f acc[C::MI][C::NJ];
+#pragma unroll
+  for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < C::NJ; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int s) {
+    const char* sbuf = lds + (s % C::kStages) * C::kStageBytes;
+    v8bf a[C::MI][2];
+#pragma unroll
+    for (int mi = 0; mi < C::MI; ++mi) {
+      const char* f = sbuf + (wm * C::MI + mi) * 2048 + lane * 16;
+      a[mi][0] = *(const v8bf*)f;
+      a[mi][1] = *(const v8bf*)(f + 1024);
+    }
+    const float sb = wsc[wn * kNIBlk + (s >> 1)];
+    v4i braw[C::NJ];
+#pragma unroll
+    for (int nj = 0; nj < C::NJ; ++nj) braw[nj] = *(const v4i*)(sbuf + C::kBOff + (wn * C::NJ + nj) * 1024 + lane * 16);
+#pragma unroll
+    for (int nj = 0; nj < C::NJ; ++nj) {
+      const v4i raw = braw[nj];
+      const v8bf b0 = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
+      const v8bf b1 = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
+#pragma unroll
+      for (int mi = 0; mi < C::MI; ++mi) {
+        v4f p = mfma_bf16_16x16x32(a[mi][0], b0, v4f{0.f, 0.f, 0.f, 0.f});
+        p = mfma_bf16_16x16x32(a[mi][1], b1, p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], sb, acc[mi][nj][i]);
+      }
+      // keep each column block's MFMA results short-lived
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Waves whose 64 rows all lie past the tile's rows only help with copies.
+  const bool wave_live = C::MI * 16 * wm < rows;
+  // copies this wave issues per stage (the same for every stage)
+  int ops_per_stage = 0;
+#pragma unroll
+  for (int k = 0; k < C::kPlanesPerWave; ++k)
+    ops_per_stage += (k >= 2 * C::kAFrags / C::kWaves || ((wave + k * C::kWaves) >> 1) * 16 < rows) ? 1 : 0;
+
+#pragma unroll
+  for (int s = 0; s < C::kStages - 1; ++s) issue(s);
+#pragma unroll 1
+  for (int s = 0; s < C::kSteps - 1; ++s) {
+    // stage s landed (stage s+1 may stay in flight); every wave has finished
+    // reading stage s-1, whose buffer takes stage s+2 after the barrier
+    wait_vmcnt_lgkm0_rt(ops_per_stage);
+    block_barrier();
+    if (s + C::kStages - 1 < C::kSteps) issue(s + C::kStages - 1);
+    if (wave_live) compute(s);
+  }
+  wait_vmcnt_lgkm0<0>();
+  block_barrier();
+  if (wave_live) compute(C::kSteps - 1);
+
+#pragma unroll
+  for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < C::NJ; ++nj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = (wm * C::MI + mi) * 16 + 4 * lq + i;
+        if (r < rows)
+          down[(size_t)(row0 + r) * kH + n0 + 16 * (wn * C::NJ + nj) + lr] = f32_to_bf16_rne(acc[mi][nj][i]);
+      }
+}
+
+hipError_t launch_gemm2_wide(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
+                             hipStream_t stream) {
+  using C = G2Wide;
+  const int64_t pairs = (int64_t)T * kTopK;
+  const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
+  const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
+  hipLaunchKernelGGL(gemm2_wide_kernel, dim3((unsigned)blocks), dim3(C::kThreads), 0, stream,
+                     (const uint16_t*)(ws + L.act), w2, w2_scale, (const int32_t*)(ws + L.expert_off),
+                     (uint16_t*)(ws + L.down));
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool gemm2_fuses_combine(int T) { return T <= kGemm2StreamMaxTokens; }
@@ -333,7 +516,7 @@ hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const L
     return hipGetLastError();
   }
   if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<1, 4, 4, 4>(T, w2, w2_scale, L, ws, stream);
-  return launch_gemm2_tiled<2, 4, 4, 4>(T, w2, w2_scale, L, ws, stream);
+  return launch_gemm2_wide(T, w2, w2_scale, L, ws, stream);
 }
 
 }  // namespace moe

@@ -179,6 +179,22 @@ __device__ __forceinline__ void wait_stages_ahead(int ahead) {
     wait_vmcnt_lgkm0<0>();
 }
 
+// s_waitcnt vmcnt(n) lgkmcnt(0) for a wave-uniform runtime n in [0, 8]
+// (larger n waits for n = 8).
+__device__ __forceinline__ void wait_vmcnt_lgkm0_rt(int n) {
+  switch (n) {
+    case 0: wait_vmcnt_lgkm0<0>(); break;
+    case 1: wait_vmcnt_lgkm0<1>(); break;
+    case 2: wait_vmcnt_lgkm0<2>(); break;
+    case 3: wait_vmcnt_lgkm0<3>(); break;
+    case 4: wait_vmcnt_lgkm0<4>(); break;
+    case 5: wait_vmcnt_lgkm0<5>(); break;
+    case 6: wait_vmcnt_lgkm0<6>(); break;
+    case 7: wait_vmcnt_lgkm0<7>(); break;
+    default: wait_vmcnt_lgkm0<8>(); break;
+  }
+}
+
 // Workgroup barrier that the compiler may not move memory accesses across.
 __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");
