@@ -112,8 +112,7 @@ typedef struct {
   size_t expert_off; /* int32 [33]     row offsets per local expert; [32] = N_sel */
   size_t perm_token; /* int32 [8T]     token of each permuted row                 */
   size_t perm_w;     /* float [8T]     combination weight of each permuted row    */
-  size_t act;        /* bf16  [8T, 2048] SwiGLU output rows; inside each group of
-                        64 columns, column 16q+8h+i is stored at 32h+8q+i       */
+  size_t act;        /* bf16  [8T, 2048] SwiGLU output rows                       */
   size_t down;       /* bf16  [8T, 7168] GEMM2 output rows                        */
   size_t block_hist; /* int32 [ceil(T/16), 32] local-expert pairs per routing workgroup */
   size_t total;      /* = moe_fp8_ds_workspace_size(T)                            */

@@ -135,7 +135,7 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
         const int prow = kDirect ? (r < rows ? inv[r] : -1) : (r < rows ? row0 + rt * 16 + r : -1);
         if (lr < 8 && prow >= 0) {
           const float silu = x2 / (1.0f + expf(-x2));
-          act[(size_t)prow * kI + act_store_col(8 * cg + lr)] = f32_to_bf16_rne(silu * v);
+          act[(size_t)prow * kI + 8 * cg + lr] = f32_to_bf16_rne(silu * v);
         }
       }
     }
@@ -178,11 +178,10 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
 //   * stages are copied global -> LDS with global_load_lds_dwordx4 (no VGPR
 //     staging) into a ring of kStages LDS buffers, the loads of stage
 //     kb + kStages - 1 in flight while stage kb is multiplied;
-//   * LDS holds each 16-row x 128-K operand fragment as two 1 KB planes in
-//     MFMA register order (lane L = 16q + r owns row r, K bytes 16q.. of plane
-//     0 and 64+16q.. of plane 1), so every ds_read_b128 of the MFMA operands is
-//     contiguous across the wave (no bank conflicts) and every DMA reads 64
-//     contiguous bytes of each of 16 rows;
+//   * LDS holds each 16-row x 128-K operand fragment as two wide 1 KB planes
+//     (8 rows x 128 B, row-major, chunks swizzled): every copy instruction
+//     reads 8 whole 128-byte row segments and the MFMA operand reads are free
+//     of bank conflicts;
 //   * per K block: P = A_f8 * B_f8 (v_mfma_f32_16x16x128_f8f6f4, exact
 //     products), acc += P * (a_scale[row] * w_scale[n/128]).
 // ---------------------------------------------------------------------------
@@ -256,15 +255,16 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
   for (int k = 0; k < C::kPlanesPerWave; ++k) {
     const int plane = wave + k * C::kWaves;
     const int frag = plane >> 1, half = plane & 1;
-    const int kofs = 16 * lq + 64 * half;  // K order of the e4m3 operands
+    int fr, chunk;
+    wide_copy_lane(lane, half, fr, chunk);
     if (frag < C::kAFrags) {
-      const int r = min(frag * 16 + lr, rows - 1);
-      src[k] = hs + (size_t)perm_token[row0 + r] * kH + kofs;
+      const int r = min(frag * 16 + fr, rows - 1);
+      src[k] = hs + (size_t)perm_token[row0 + r] * kH + 16 * chunk;
       dst[k] = frag * C::kFrag + half * 1024;
     } else {
       const int bf = frag - C::kAFrags;
-      const int n = bf < 2 * WN ? j0 + 16 * bf + lr : kI + j0 + 16 * (bf - 2 * WN) + lr;
-      src[k] = w13 + ((size_t)e * k2I + n) * kH + kofs;
+      const int n = bf < 2 * WN ? j0 + 16 * bf + fr : kI + j0 + 16 * (bf - 2 * WN) + fr;
+      src[k] = w13 + ((size_t)e * k2I + n) * kH + 16 * chunk;
       dst[k] = C::kBOff + bf * C::kFrag + half * 1024;
     }
   }
@@ -304,9 +304,10 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
     v4f sa[MI];
     float sg, su;
   };
+  const int slot_lo = wide_slot(lr, 2 * lq), slot_hi = wide_slot(lr, 2 * lq + 1);
   auto frag = [&](int s, int off) {
-    const char* f = lds + (s % C::kStages) * C::kStageBytes + off + lane * 16;
-    const v4i lo = *(const v4i*)f, hi = *(const v4i*)(f + 1024);
+    const char* f = lds + (s % C::kStages) * C::kStageBytes + off;
+    const v4i lo = *(const v4i*)(f + slot_lo), hi = *(const v4i*)(f + slot_hi);
     return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
   auto read_b = [&](int s, Frags& F) {
@@ -399,7 +400,7 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
         if (r < rows) {
           const float x1 = acc[mi][nj][i], x2 = acc[mi][nj + 2][i];
           const float silu = x2 / (1.0f + expf(-x2));
-          act[(size_t)(row0 + r) * kI + act_store_col(j0 + 32 * wn + 16 * nj + lr)] = f32_to_bf16_rne(silu * x1);
+          act[(size_t)(row0 + r) * kI + j0 + 32 * wn + 16 * nj + lr] = f32_to_bf16_rne(silu * x1);
         }
       }
 }
@@ -487,6 +488,7 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
   const int lr = lane & 15;
   const int wm = wave / C::WN;
   const int wn = wave % C::WN;
+  const int slot_lo = wide_slot(lr, 2 * lq), slot_hi = wide_slot(lr, 2 * lq + 1);
 
   // ---- DMA planes of this wave: planes wave + 8k; k < 4 are A, k >= 4 are B
   const uint8_t* w13e = w13 + (size_t)e * k2I * kH;
@@ -496,15 +498,16 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
   for (int k = 0; k < C::kPlanesPerWave; ++k) {
     const int plane = wave + k * C::kWaves;
     const int frag = plane >> 1, half = plane & 1;
-    const uint32_t kofs = 16 * lq + 64 * half;  // K order of the e4m3 operands
+    int fr, chunk;
+    wide_copy_lane(lane, half, fr, chunk);
     if (frag < C::kAFrags) {
-      const int r = min(frag * 16 + lr, rows - 1);
-      off[k] = (uint32_t)perm_token[row0 + r] * kH + kofs;
+      const int r = min(frag * 16 + fr, rows - 1);
+      off[k] = (uint32_t)perm_token[row0 + r] * kH + 16 * chunk;
       dst[k] = frag * C::kFrag + half * 1024;
     } else {
       const int bf = frag - C::kAFrags;  // 0..7 gate, 8..15 up
-      const int n = bf < 8 ? j0 + 16 * bf + lr : kI + j0 + 16 * (bf - 8) + lr;
-      off[k] = (uint32_t)n * kH + kofs;
+      const int n = bf < 8 ? j0 + 16 * bf + fr : kI + j0 + 16 * (bf - 8) + fr;
+      off[k] = (uint32_t)n * kH + 16 * chunk;
       dst[k] = C::kBOff + bf * C::kFrag + half * 1024;
     }
   }
@@ -540,8 +543,8 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
   auto compute = [&](int kb) {
     const char* sb = lds + (kb & 1) * C::kStageBytes;
     auto frag = [&](int off_) {
-      const char* f = sb + off_ + lane * 16;
-      const v4i lo = *(const v4i*)f, hi = *(const v4i*)(f + 1024);
+      const char* f = sb + off_;
+      const v4i lo = *(const v4i*)(f + slot_lo), hi = *(const v4i*)(f + slot_hi);
       return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
     v8i b[2 * C::NJ];
@@ -606,7 +609,7 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
         if (r < rows) {
           const float x1 = acc[mi][nj][i], x2 = acc[mi][C::NJ + nj][i];
           const float silu = x2 / (1.0f + expf(-x2));
-          act[(size_t)(row0 + r) * kI + act_store_col(j0 + 16 * (C::NJ * wn + nj) + lr)] = f32_to_bf16_rne(silu * x1);
+          act[(size_t)(row0 + r) * kI + j0 + 16 * (C::NJ * wn + nj) + lr] = f32_to_bf16_rne(silu * x1);
         }
       }
 }

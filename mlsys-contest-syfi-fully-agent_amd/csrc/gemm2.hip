@@ -54,7 +54,7 @@ __device__ __forceinline__ S2Job s2_next(const ExpertRows& X, uint32_t active, S
 
 struct S2Regs {
   v4i b[kS2KB][2];     // e4m3 W2 row bytes 64g + 16q .. +15 of each scale block
-  v4i a[kS2KB][2][2];  // bf16 act (stored order): elements 64g + 32h + 8q .. +7
+  v4i a[kS2KB][2][2];  // bf16 act: elements 64g + 16q + 8h .. +7
   float sw[kS2KB];
   int tok;           // token and weight of the row this thread combines
   float pw;          //   (threads < 256: row = tid / 16 of the tile)
@@ -71,14 +71,14 @@ __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
   R.tok = perm_token[crow];
   R.pw = perm_w[crow];
   const uint8_t* bp = w2 + ((size_t)j.e * kH + n0 + lr) * kI + kb0 * kBlk + 16 * lq;
-  const uint16_t* ap = act + (size_t)(row0 + min(lr, rows - 1)) * kI + kb0 * kBlk + 8 * lq;
+  const uint16_t* ap = act + (size_t)(row0 + min(lr, rows - 1)) * kI + kb0 * kBlk + 16 * lq;
 #pragma unroll
   for (int k = 0; k < kS2KB; ++k) {
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       R.b[k][g] = *(const v4i*)(bp + k * kBlk + 64 * g);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) R.a[k][g][h] = *(const v4i*)(ap + k * kBlk + 64 * g + 32 * h);
+      for (int h = 0; h < 2; ++h) R.a[k][g][h] = *(const v4i*)(ap + k * kBlk + 64 * g + 8 * h);
     }
     R.sw[k] = w2_scale[((size_t)j.e * kNHBlk + n0 / kBlk) * kNIBlk + kb0 + k];
   }
@@ -152,11 +152,11 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
 //   * a pipeline stage is 64 K values: the bf16 activation rows (A) and the
 //     e4m3 W2 rows (B), copied global -> LDS by global_load_lds_dwordx4,
 //     4 LDS buffers (loads for stage s+3 in flight while stage s multiplies);
-//   * operand fragments sit in LDS in MFMA register order: an A fragment
-//     (16 rows x 64 K bf16) is two 1 KB planes, a B fragment (16 rows x 64 K
-//     e4m3) one plane; lane L = 16*q + r owns row r, K = 16q .. 16q+15 of the
-//     stage, instruction j taking K = 16q + 8j .. +7 (the act columns are
-//     stored so that these are 16 contiguous bytes: act_store_col);
+//   * operand fragments sit in LDS row-major with swizzled chunks: an A
+//     fragment (16 rows x 64 K bf16 = 128 B per row) is two wide planes, a B
+//     fragment (16 rows x 64 K e4m3) one narrow plane; MFMA lane L = 16*q + r
+//     works on row r, K = 16q .. 16q+15 of the stage, instruction j taking
+//     K = 16q + 8j .. +7;
 //   * B is widened e4m3 -> bf16 exactly in registers (v_cvt_scalef32_pk_bf16_fp8
 //     with scale 1); P accumulates the two stages of a 128-K scale block on
 //     v_mfma_f32_16x16x32_bf16, then acc += P * w_scale[n/128, kb].
@@ -213,6 +213,8 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
   const int lr = lane & 15;
   const int wm = wave / WN;
   const int wn = wave % WN;
+  // MFMA operand slots: A rows in wide layout (chunks 2q, 2q+1), B rows narrow (chunk q)
+  const int slot_a0 = wide_slot(lr, 2 * lq), slot_a1 = wide_slot(lr, 2 * lq + 1), slot_b = narrow_slot(lr, lq);
 
   // per-lane DMA sources at stage 0 (byte pointers) and LDS destinations
   const char* src[C::kPlanesPerWave];
@@ -222,12 +224,16 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
     const int plane = wave + k * C::kWaves;
     if (plane < 2 * C::kAFrags) {
       const int f = plane >> 1, p = plane & 1;
-      const int r = min(f * 16 + lr, rows - 1);
-      src[k] = (const char*)(act + (size_t)(row0 + r) * kI + 32 * p + 8 * lq);  // stored order
+      int fr, chunk;
+      wide_copy_lane(lane, p, fr, chunk);
+      const int r = min(f * 16 + fr, rows - 1);
+      src[k] = (const char*)(act + (size_t)(row0 + r) * kI + 8 * chunk);
       dst[k] = f * 2048 + p * 1024;
     } else {
       const int f = plane - 2 * C::kAFrags;
-      src[k] = (const char*)(w2 + ((size_t)e * kH + n0 + 16 * f + lr) * kI + 16 * lq);
+      int fr, chunk;
+      narrow_copy_lane(lane, fr, chunk);
+      src[k] = (const char*)(w2 + ((size_t)e * kH + n0 + 16 * f + fr) * kI + 16 * chunk);
       dst[k] = C::kBOff + f * 1024;
     }
   }
@@ -265,13 +271,13 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
     v8bf a[MI][2], b[NJ][2];
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      const char* f = sbuf + (wm * MI + mi) * 2048 + lane * 16;
-      a[mi][0] = *(const v8bf*)f;
-      a[mi][1] = *(const v8bf*)(f + 1024);
+      const char* f = sbuf + (wm * MI + mi) * 2048;
+      a[mi][0] = *(const v8bf*)(f + slot_a0);
+      a[mi][1] = *(const v8bf*)(f + slot_a1);
     }
 #pragma unroll
     for (int nj = 0; nj < NJ; ++nj) {
-      const v4i raw = *(const v4i*)(sbuf + C::kBOff + (wn * NJ + nj) * 1024 + lane * 16);
+      const v4i raw = *(const v4i*)(sbuf + C::kBOff + (wn * NJ + nj) * 1024 + slot_b);
       b[nj][0] = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
       b[nj][1] = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
     }
@@ -379,6 +385,8 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
   const int lr = lane & 15;
   const int wm = wave / C::WN;
   const int wn = wave % C::WN;
+  // MFMA operand slots: A rows in wide layout (chunks 2q, 2q+1), B rows narrow (chunk q)
+  const int slot_a0 = wide_slot(lr, 2 * lq), slot_a1 = wide_slot(lr, 2 * lq + 1), slot_b = narrow_slot(lr, lq);
 
   // DMA planes wave + 8k: k < 4 are A planes (bf16 act rows), k >= 4 B planes
   const char* actb = (const char*)(act + (size_t)row0 * kI);
@@ -390,12 +398,16 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
     const int plane = wave + k * C::kWaves;
     if (plane < 2 * C::kAFrags) {
       const int f = plane >> 1, p = plane & 1;
-      const int r = min(f * 16 + lr, rows - 1);
-      off[k] = (uint32_t)(r * kI + 32 * p + 8 * lq) * 2;  // stored order
+      int fr, chunk;
+      wide_copy_lane(lane, p, fr, chunk);
+      const int r = min(f * 16 + fr, rows - 1);
+      off[k] = (uint32_t)(r * kI + 8 * chunk) * 2;
       dst[k] = f * 2048 + p * 1024;
     } else {
       const int f = plane - 2 * C::kAFrags;
-      off[k] = (uint32_t)(n0 + 16 * f + lr) * kI + 16 * lq;
+      int fr, chunk;
+      narrow_copy_lane(lane, fr, chunk);
+      off[k] = (uint32_t)(n0 + 16 * f + fr) * kI + 16 * chunk;
       dst[k] = C::kBOff + f * 1024;
     }
   }
@@ -431,14 +443,14 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
     v8bf a[C::MI][2];
 #pragma unroll
     for (int mi = 0; mi < C::MI; ++mi) {
-      const char* f = sbuf + (wm * C::MI + mi) * 2048 + lane * 16;
-      a[mi][0] = *(const v8bf*)f;
-      a[mi][1] = *(const v8bf*)(f + 1024);
+      const char* f = sbuf + (wm * C::MI + mi) * 2048;
+      a[mi][0] = *(const v8bf*)(f + slot_a0);
+      a[mi][1] = *(const v8bf*)(f + slot_a1);
     }
     const float sb = wsc[wn * kNIBlk + (s >> 1)];
     v4i braw[C::NJ];
 #pragma unroll
-    for (int nj = 0; nj < C::NJ; ++nj) braw[nj] = *(const v4i*)(sbuf + C::kBOff + (wn * C::NJ + nj) * 1024 + lane * 16);
+    for (int nj = 0; nj < C::NJ; ++nj) braw[nj] = *(const v4i*)(sbuf + C::kBOff + (wn * C::NJ + nj) * 1024 + slot_b);
 #pragma unroll
     for (int nj = 0; nj < C::NJ; ++nj) {
       const v4i raw = braw[nj];

@@ -57,23 +57,41 @@ inline Layout make_layout(int64_t T) {
 }
 
 // ---------------------------------------------------------------------------
-// Operand K order.  An MFMA sums over K, so any permutation of K that A and B
-// share leaves each dot product unchanged; the kernels pick the one that
-// makes every 16-byte load part of a 64-byte contiguous run per row (a 32-byte
-// stride between the pieces of a row costs ~3x in L2 -> LDS throughput).
-//   * e4m3 operands of the tiled GEMM1 (16x16x128 MFMA): the lane at quarter
-//     q (lanes 16q..16q+15) holds K bytes 16q..16q+15 and 64+16q..64+16q+15
-//     of the 128-K block (the streaming GEMM1 keeps 32q..32q+31: its weights
-//     stream from HBM, where that order measured faster);
-//   * bf16 activation rows (`act`, written by GEMM1, read by GEMM2): inside
-//     each group of 64 columns, logical column 16q + 8h + i (q < 4, h < 2,
-//     i < 8) is stored at 32h + 8q + i, so the 16 bytes stored at 32h + 8q ..
-//     (one contiguous load) are the K indices that pair with the h-th half of
-//     the 16 weight bytes a GEMM2 lane loads at 16q.
+// LDS operand tiles.  A 16-row MFMA fragment is staged in LDS row-major:
+//   * wide: 128 bytes of K per row, two 1 KB planes of 8 rows each;
+//   * narrow: 64 bytes of K per row, one 1 KB plane of 16 rows.
+// Tiles are copied global -> LDS with global_load_lds_dwordx4, where lane i
+// of a copy always writes bytes 16i .. 16i+15 of its plane.  Lane i is given
+// the (row, 16-byte chunk) that makes
+//   * 8 (wide) or 4 (narrow) consecutive lanes read one row's 128 or 64
+//     contiguous bytes -- the vector memory path coalesces consecutive lanes,
+//     and a copy whose consecutive lanes touch different rows runs at about
+//     half the L2 -> LDS rate;
+//   * chunk c of row r land at slot c ^ swz(r), so that the MFMA operand
+//     reads, where the 16 lanes of a quarter read 16 rows at the same logical
+//     chunk, fall on 16 distinct 16-byte bank groups.
+// MFMA lane (q = lane / 16, r = lane % 16) reads row r at logical chunks
+//   * wide: 2q and 2q + 1 (K bytes 32q .. 32q+31 of the row);
+//   * narrow: q (K bytes 16q .. 16q+15).
+// Both operands of an MFMA use the same mapping, so K is in natural order and
+// the bf16 activation rows are stored in natural column order.
 // ---------------------------------------------------------------------------
-__host__ __device__ constexpr int act_store_col(int c) {
-  return (c & ~63) + 32 * ((c >> 3) & 1) + 8 * ((c >> 4) & 3) + (c & 7);
+__device__ __forceinline__ int swz_wide(int r) { return (r & 7) ^ (r >> 3); }  // r < 16
+__device__ __forceinline__ int swz_narrow(int r) { return (r >> 2) & 3; }      // r < 16
+
+// Copy lane -> (row of the fragment, source chunk) for wide plane `half`.
+__device__ __forceinline__ void wide_copy_lane(int lane, int half, int& row, int& chunk) {
+  row = 8 * half + (lane >> 3);
+  chunk = (lane & 7) ^ swz_wide(row);
 }
+// Copy lane -> (row, source chunk) for a narrow plane.
+__device__ __forceinline__ void narrow_copy_lane(int lane, int& row, int& chunk) {
+  row = lane >> 2;
+  chunk = (lane & 3) ^ swz_narrow(row);
+}
+// Byte offset of (row r, logical chunk c) inside a wide fragment / narrow plane.
+__device__ __forceinline__ int wide_slot(int r, int c) { return 1024 * (r >> 3) + 128 * (r & 7) + 16 * (c ^ swz_wide(r)); }
+__device__ __forceinline__ int narrow_slot(int r, int c) { return 64 * r + 16 * (c ^ swz_narrow(r)); }
 
 // ---------------------------------------------------------------------------
 // device helpers

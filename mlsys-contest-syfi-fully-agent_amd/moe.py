@@ -106,17 +106,6 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_
     return output
 
 
-def act_store_columns():
-    """Stored position of each logical column of the workspace's activation
-    rows (`act`): inside each group of 64 columns, logical 16q + 8h + i is
-    stored at 32h + 8q + i (act_store_col in csrc/moe_common.hpp).  Use as
-    ``act[:, act_store_columns()]`` to get logical order."""
-    import numpy as np
-
-    c = np.arange(I)
-    return (c & ~63) + 32 * ((c >> 3) & 1) + 8 * ((c >> 4) & 3) + (c & 7)
-
-
 class RouteResult:
     """Typed views of the routing/permutation regions of a workspace."""
 

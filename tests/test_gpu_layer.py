@@ -121,7 +121,6 @@ def test_intermediates_match_oracle(pkg, orc, cuda_device, name, T, n_rows):
         rng = np.random.default_rng(n)
         sel = np.unique(np.concatenate([edges, rng.choice(n, n_rows, replace=False)]))
     act = (r.act[sel].cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
-    act = act[:, pkg.moe.act_store_columns()]  # stored column order -> logical
     down = (r.down[sel].cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
     x = oracle_inputs(cfg, host, w_host)
     c_ref, o_ref = orc.expert_rows(x, perm[sel], le_all[sel])
