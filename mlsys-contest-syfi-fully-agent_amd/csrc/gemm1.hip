@@ -185,7 +185,9 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
 //   * per K block: P = A_f8 * B_f8 (v_mfma_f32_16x16x128_f8f6f4, exact
 //     products), acc += P * (a_scale[row] * w_scale[n/128]).
 // ---------------------------------------------------------------------------
-// Token count from which GEMM1 uses 256-row tiles (below: 64-row tiles).
+// Token count from which GEMM1 uses the wide 256 x 256 tiles.  Below it,
+// experts have few rows, and 64-row x 64-gate-column tiles of 8 waves give
+// more workgroups to stream the weights (measured fastest at T = 1024).
 constexpr int kGemm1TiledLargeMinTokens = 2048;
 
 template <int WM, int WN, int MI>
@@ -643,7 +645,7 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const u
                          hs, hs_scale, T, w13, w13_scale, off, perm, act);
     return hipGetLastError();
   }
-  if (T < kGemm1TiledLargeMinTokens) return launch_gemm1_tiled<1, 4, 4>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
+  if (T < kGemm1TiledLargeMinTokens) return launch_gemm1_tiled<4, 2, 1>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
   return launch_gemm1_wide(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
 }
 

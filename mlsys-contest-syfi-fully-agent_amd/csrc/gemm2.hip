@@ -161,7 +161,8 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
 //     with scale 1); P accumulates the two stages of a 128-K scale block on
 //     v_mfma_f32_16x16x32_bf16, then acc += P * w_scale[n/128, kb].
 // ---------------------------------------------------------------------------
-// Token count from which GEMM2 uses 128-row tiles (below: 64-row tiles).
+// Token count from which GEMM2 uses the wide 256 x 256 tiles (below: 64 x 128
+// tiles of 8 waves, measured fastest at T = 1024).
 constexpr int kGemm2TiledLargeMinTokens = 2048;
 
 template <int WM, int WN, int MI, int NJ>
@@ -527,7 +528,7 @@ hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const L
                        (const int32_t*)(ws + L.perm_token), (const float*)(ws + L.perm_w), T, (uint16_t*)out);
     return hipGetLastError();
   }
-  if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<1, 4, 4, 4>(T, w2, w2_scale, L, ws, stream);
+  if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<2, 4, 2, 2>(T, w2, w2_scale, L, ws, stream);
   return launch_gemm2_wide(T, w2, w2_scale, L, ws, stream);
 }
 

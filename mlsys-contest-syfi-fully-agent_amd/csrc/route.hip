@@ -37,62 +37,40 @@ constexpr int kDppQuad2301 = 0x4E;    // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
 constexpr int kDppRowBcast15 = 0x142;
-constexpr int kDppRowBcast31 = 0x143;
 
 template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   // lanes outside ROW_MASK keep their own value (old = v)
-  const uint32_t l2 = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, CTRL, ROW_MASK, 0xF, false);
-  const uint32_t h2 = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, CTRL, ROW_MASK, 0xF, false);
-  return ((uint64_t)h2 << 32) | l2;
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROW_MASK, 0xF, false);
 }
 
-// Maximum over each row of 16 lanes, in every lane of the row.
-__device__ __forceinline__ uint64_t row_max(uint64_t k) {
-  k = u64max(k, dpp_u64<kDppQuad1032, 0xF>(k));
-  k = u64max(k, dpp_u64<kDppQuad2301, 0xF>(k));
-  k = u64max(k, dpp_u64<kDppRowHalfMirror, 0xF>(k));
-  k = u64max(k, dpp_u64<kDppRowMirror, 0xF>(k));
-  return k;
+// Maxima of the two half-waves (lanes 0-31, 32-63) of a 32-bit key,
+// wave-uniform.  Four DPP row steps, then rows 1 and 3 take rows 0 and 2.
+__device__ __forceinline__ void halfwave_max(uint32_t k, uint32_t& m0, uint32_t& m1) {
+  k = max(k, dpp_u32<kDppQuad1032, 0xF>(k));
+  k = max(k, dpp_u32<kDppQuad2301, 0xF>(k));
+  k = max(k, dpp_u32<kDppRowHalfMirror, 0xF>(k));
+  k = max(k, dpp_u32<kDppRowMirror, 0xF>(k));
+  k = max(k, dpp_u32<kDppRowBcast15, 0xA>(k));
+  m0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 31);
+  m1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
 }
 
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int lane) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// Maxima of the two half-waves (lanes 0-31, 32-63), wave-uniform.
-__device__ __forceinline__ void halfwave_max(uint64_t k, uint64_t& m0, uint64_t& m1) {
-  k = row_max(k);
-  k = u64max(k, dpp_u64<kDppRowBcast15, 0xA>(k));  // rows 1, 3 see rows 0, 2
-  m0 = readlane_u64(k, 31);
-  m1 = readlane_u64(k, 63);
-}
-
-// Maximum over the wave, wave-uniform.
-__device__ __forceinline__ uint64_t wave_max(uint64_t k) {
-  k = row_max(k);
-  k = u64max(k, dpp_u64<kDppRowBcast15, 0xA>(k));
-  k = u64max(k, dpp_u64<kDppRowBcast31, 0xC>(k));
-  return readlane_u64(k, 63);
-}
-
-__device__ __forceinline__ uint64_t make_key(float v, int e) {
-  return ((uint64_t)float_order_key(v) << 32) | (uint32_t)(255 - e);
-}
-
-__device__ __forceinline__ float key_value(uint64_t k) { return float_from_order_key((uint32_t)(k >> 32)); }
+__device__ __forceinline__ int popc_ballot(bool p) { return __popcll(__ballot(p)); }
 
 // Routes token t with one wavefront.  Returns the 8 selected ids, ascending
-// (wave-uniform), and writes ids / weights.
+// (wave-uniform), and their weights (wave-uniform).
+//
+// Lane l holds experts l, l+64, l+128, l+192 (slot j = expert / 64); the
+// routing group of 32 experts g = 2j + (l >= 32) is one half-wave of one slot.
+// Scores are compared through 32-bit order-preserving keys of the fp32 values
+// (masked experts: key 0, below every real score); among equal scores the
+// lower expert index wins.
 __device__ void route_token(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
-                            float rsf, int t, int32_t* __restrict__ ids_out,
-                            float* __restrict__ w_out, int sel[kTopK]) {
+                            float rsf, int t, int sel[kTopK], float wsel[kTopK]) {
   const int lane = threadIdx.x & (kWave - 1);
   float s[4];
-  uint64_t key[4];
+  uint32_t key[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = 64 * j + lane;
@@ -101,19 +79,24 @@ __device__ void route_token(const float* __restrict__ logits, const uint16_t* __
     const float ex = (float)exp(-(double)x);
     s[j] = 1.0f / (1.0f + ex);
     // moe.py:128: s_with_bias = s + bias
-    key[j] = make_key(s[j] + bf16_to_f32(bias[e]), e);
+    key[j] = float_order_key(s[j] + bf16_to_f32(bias[e]));
   }
-  // moe.py:135-136: group score = sum of the two largest biased scores.
-  // Slot j, half h holds group 2j + h.
+  // moe.py:135-136: group score = sum of the two largest biased scores (a
+  // repeated maximum counts twice).  The four slots reduce independently.
   float G[kNGroup];
+  uint32_t m1[4][2], m2[4][2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) halfwave_max(key[j], m1[j][0], m1[j][1]);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    uint64_t a0, a1, b0, b1;
-    halfwave_max(key[j], a0, a1);
-    const uint64_t own = (lane < 32) ? a0 : a1;
-    halfwave_max(key[j] == own ? 0ull : key[j], b0, b1);
-    G[2 * j] = key_value(a0) + key_value(b0);
-    G[2 * j + 1] = key_value(a1) + key_value(b1);
+    const uint32_t mine = lane < 32 ? m1[j][0] : m1[j][1];
+    const uint64_t eq = __ballot(key[j] == mine);
+    // drop one instance of the maximum (the lowest lane holding it)
+    const int lo0 = __builtin_ctzll(eq & 0x00000000FFFFFFFFull);
+    const int lo1 = __builtin_ctzll(eq & 0xFFFFFFFF00000000ull);
+    halfwave_max(lane == lo0 || lane == lo1 ? 0u : key[j], m2[j][0], m2[j][1]);
+    G[2 * j] = float_from_order_key(m1[j][0]) + float_from_order_key(m2[j][0]);
+    G[2 * j + 1] = float_from_order_key(m1[j][1]) + float_from_order_key(m2[j][1]);
   }
   // moe.py:139-146: keep the top-4 groups (ties -> lower group index).
   uint32_t keep = 0;
@@ -124,54 +107,59 @@ __device__ void route_token(const float* __restrict__ logits, const uint16_t* __
     for (int h = 0; h < kNGroup; ++h) rank += (G[h] > G[g]) || (G[h] == G[g] && h < g);
     keep |= (rank < kTopKGroup ? 1u : 0u) << g;
   }
-  // moe.py:149-151: top-8 experts among the kept groups.
+  // moe.py:149-151: top-8 experts among the kept groups.  theta = the 8th
+  // largest key (radix select: the largest value v with count(key >= v) >= 8,
+  // one bit at a time from the top); take every key > theta and, of the keys
+  // equal to theta, the lowest expert indices.
   const int half = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    if (!((keep >> (2 * j + half)) & 1u)) key[j] = 0ull;
+    if (!((keep >> (2 * j + half)) & 1u)) key[j] = 0u;
+  uint32_t theta = 0;
+#pragma unroll
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = theta | (1u << b);
+    const int cnt = popc_ballot(key[0] >= cand) + popc_ballot(key[1] >= cand) + popc_ballot(key[2] >= cand) +
+                    popc_ballot(key[3] >= cand);
+    if (cnt >= kTopK) theta = cand;
+  }
+  uint64_t pick[4];
+  int need = kTopK;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    pick[j] = __ballot(key[j] > theta);
+    need -= __popcll(pick[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint64_t eq = __ballot(key[j] == theta);
+    while (need > 0 && eq) {
+      pick[j] |= eq & (~eq + 1);  // lowest remaining lane
+      eq &= eq - 1;
+      --need;
+    }
+  }
+  // ids ascending = slot-major, lane-minor order of the picked bits (all
+  // wave-uniform; the loop is unrolled so every index is static)
 #pragma unroll
   for (int r = 0; r < kTopK; ++r) {
-    const uint64_t m = wave_max(u64max(u64max(key[0], key[1]), u64max(key[2], key[3])));
-    sel[r] = 255 - (int)(uint32_t)(m & 0xFFu);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (key[j] == m) key[j] = 0ull;
+    const int j = pick[0] ? 0 : pick[1] ? 1 : pick[2] ? 2 : 3;
+    const uint64_t m = j == 0 ? pick[0] : j == 1 ? pick[1] : j == 2 ? pick[2] : pick[3];
+    const int l = m ? __builtin_ctzll(m) : 0;  // m != 0 whenever 8 keys are nonzero
+    const uint64_t rest = m & (m - 1);
+    if (j == 0) pick[0] = rest; else if (j == 1) pick[1] = rest; else if (j == 2) pick[2] = rest; else pick[3] = rest;
+    sel[r] = 64 * j + l;
+    const float sj = j == 0 ? s[0] : j == 1 ? s[1] : j == 2 ? s[2] : s[3];
+    wsel[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), l));
   }
-  // ascending ids (wave-uniform values)
-#pragma unroll
-  for (int a = 1; a < kTopK; ++a)
-#pragma unroll
-    for (int b = kTopK - 1; b >= a; --b)
-      if (sel[b - 1] > sel[b]) {
-        const int tmp = sel[b];
-        sel[b] = sel[b - 1];
-        sel[b - 1] = tmp;
-      }
   // moe.py:154-158: weights from the un-biased sigmoid, summed in ascending id
   // order, normalised (true division) then scaled.
-  float sv[kTopK];
   float sum = 0.0f;
 #pragma unroll
-  for (int r = 0; r < kTopK; ++r) {
-    const int e = sel[r];
-    const int j = e >> 6;
-    const float mine = j == 0 ? s[0] : j == 1 ? s[1] : j == 2 ? s[2] : s[3];
-    sv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), e & 63));
-    sum = sum + sv[r];
-  }
+  for (int k = 0; k < kTopK; ++k) sum = sum + wsel[k];
   const float denom = sum + 1e-20f;
-  if (lane < kTopK) {
-    float mys = sv[0];
-    int mye = sel[0];
 #pragma unroll
-    for (int r = 1; r < kTopK; ++r)
-      if (lane == r) {
-        mys = sv[r];
-        mye = sel[r];
-      }
-    ids_out[(size_t)t * kTopK + lane] = mye;
-    w_out[(size_t)t * kTopK + lane] = (mys / denom) * rsf;
-  }
+  for (int k = 0; k < kTopK; ++k) wsel[k] = (wsel[k] / denom) * rsf;
 }
 
 // Local-expert bitmask of a token's 8 ascending ids, and the slot of its first
@@ -286,45 +274,86 @@ __device__ void scatter_chunk(const int32_t* __restrict__ ids, const float* __re
 }
 
 // Routing of 16 tokens per workgroup.  With a single workgroup (T <= 16) it
-// also builds the permutation; otherwise it writes its local-expert histogram
-// to block_hist[blockIdx.x][32] for perm_kernel.
+// also builds the permutation, from LDS only (no global round trip of the
+// ids); otherwise it writes its local-expert histogram to
+// block_hist[blockIdx.x][32] for perm_kernel.
 __global__ void __launch_bounds__(kRouteThreads)
 route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf, int T,
              int64_t offset, int32_t* __restrict__ ids, float* __restrict__ w,
              int32_t* __restrict__ pair_row, int32_t* __restrict__ expert_off,
              int32_t* __restrict__ perm_token, float* __restrict__ perm_w, int32_t* __restrict__ block_hist) {
   __shared__ int hist[kELocal];
-  if (threadIdx.x < kELocal) hist[threadIdx.x] = 0;
+  __shared__ uint32_t tokmask[kELocal];  // bit w: this workgroup's token w chose local expert
+  __shared__ int first_row[kELocal];
+  __shared__ int pair_id[kRouteWaves][kTopK];
+  __shared__ float pair_w[kRouteWaves][kTopK];
+  if (threadIdx.x < kELocal) {
+    hist[threadIdx.x] = 0;
+    tokmask[threadIdx.x] = 0u;
+  }
   __syncthreads();
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int t = blockIdx.x * kRouteWaves + threadIdx.x / kWave;
+  const int tw = threadIdx.x / kWave;
+  const int t = blockIdx.x * kRouteWaves + tw;
   if (t < T) {
     int sel[kTopK];
-    route_token(logits, bias, rsf, t, ids, w, sel);
+    float wsel[kTopK];
+    route_token(logits, bias, rsf, t, sel, wsel);
     if (lane < kTopK) {
       int e = sel[0];
+      float we = wsel[0];
 #pragma unroll
       for (int r = 1; r < kTopK; ++r)
-        if (lane == r) e = sel[r];
+        if (lane == r) {
+          e = sel[r];
+          we = wsel[r];
+        }
+      ids[(size_t)t * kTopK + lane] = e;
+      w[(size_t)t * kTopK + lane] = we;
+      pair_id[tw][lane] = e;
+      pair_w[tw][lane] = we;
       const int64_t le = (int64_t)e - offset;
-      if (le >= 0 && le < kELocal) atomicAdd(&hist[(int)le], 1);
+      if (le >= 0 && le < kELocal) {
+        atomicAdd(&hist[(int)le], 1);
+        atomicOr(&tokmask[(int)le], 1u << tw);
+      }
     }
   }
-  __syncthreads();  // also makes this block's ids visible to all its threads
+  __syncthreads();
   if (gridDim.x > 1) {
     if (threadIdx.x < kELocal) block_hist[(size_t)blockIdx.x * kELocal + threadIdx.x] = hist[threadIdx.x];
     return;
   }
-  __shared__ PermShared sh;
-  if (threadIdx.x < kELocal) {
-    sh.total[threadIdx.x] = hist[threadIdx.x];
-    sh.before[threadIdx.x] = 0;
+  // T <= 16: rows of expert le are its tokens in ascending order, starting at
+  // the exclusive scan of the per-expert counts.
+  if (threadIdx.x < kWave) {
+    const int c = lane < kELocal ? __popc(tokmask[lane]) : 0;
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < kELocal; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += v;
+    }
+    if (lane < kELocal) {
+      first_row[lane] = incl - c;
+      expert_off[lane] = incl - c;
+      if (lane == kELocal - 1) expert_off[kELocal] = incl;
+    }
   }
   __syncthreads();
-  if (threadIdx.x < kWave) expert_offsets(sh, true, expert_off);
-  __syncthreads();
-  scatter_chunk(ids, w, T, 0, offset, sh, pair_row, perm_token, perm_w);
+  const int p = threadIdx.x;  // pair p = (token p / 8, slot p % 8)
+  if (p < T * kTopK) {
+    const int pt = p / kTopK, k = p % kTopK;
+    const int64_t le = (int64_t)pair_id[pt][k] - offset;
+    int row = -1;
+    if (le >= 0 && le < kELocal) {
+      row = first_row[le] + __popc(tokmask[le] & ((1u << pt) - 1u));
+      perm_token[row] = pt;
+      perm_w[row] = pair_w[pt][k];
+    }
+    pair_row[p] = row;
+  }
 }
 
 // Permutation for T > 16: workgroup c handles tokens [1024c, 1024c + 1024).
