@@ -10,12 +10,13 @@
 //   * one wavefront per token, 16 tokens per 1024-thread workgroup; lane l
 //     owns experts l, l+64, l+128, l+192, so a routing group of 32 experts is
 //     one half-wave in one register slot;
-//   * scores are packed into 64-bit keys (order-preserving float bits, then
-//     255 - expert) so one max-reduction gives value and lowest-index
-//     tie-break at once; reductions use DPP lane movements (VALU latency, no
-//     LDS round trips);
-//   * T <= 16 (decode): the single workgroup also builds the permutation, with
-//     no global atomics or fences;
+//   * scores become 32-bit order-preserving keys; the group top-2 sums use
+//     DPP max-reductions per half-wave (four slots in parallel), and the
+//     top-8 is a radix select on the keys (one ballot count per bit) followed
+//     by ballots that take the tied keys in ascending expert order;
+//   * T <= 16 (decode): the single workgroup also builds the permutation from
+//     LDS (per-expert token bitmasks), with no global atomics, fences or
+//     re-reads of the ids;
 //   * larger T: each workgroup stores its local-expert histogram (plain
 //     stores, no atomics); a second kernel (one workgroup per 1024 tokens)
 //     reduces the histograms to the expert row offsets and the per-chunk bases
