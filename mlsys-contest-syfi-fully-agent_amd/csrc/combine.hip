@@ -16,12 +16,17 @@
 namespace moe {
 namespace {
 
-constexpr int kCombThreads = 256;
+// 448 threads x 16 columns = one 7168-column row per workgroup; every lane
+// issues its (up to 8 rows x 2) 16-byte loads before the first add.
+constexpr int kCombThreads = 448;
+constexpr int kCombCols = 16;
+static_assert(kCombThreads * kCombCols == kH, "one row per workgroup");
 
 __global__ void __launch_bounds__(kCombThreads)
 combine_kernel(const uint16_t* __restrict__ down, const int32_t* __restrict__ pair_row,
                const float* __restrict__ topk_w, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
+  const int c = threadIdx.x * kCombCols;
   int row[kTopK];
   float w[kTopK];
 #pragma unroll
@@ -29,22 +34,43 @@ combine_kernel(const uint16_t* __restrict__ down, const int32_t* __restrict__ pa
     row[k] = pair_row[(size_t)t * kTopK + k];
     w[k] = topk_w[(size_t)t * kTopK + k];
   }
-  for (int c = threadIdx.x * 4; c < kH; c += kCombThreads * 4) {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  uint4 v[kTopK][2];
 #pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-      if (row[k] < 0) continue;
-      const uint2 v = *(const uint2*)(down + (size_t)row[k] * kH + c);
-      a0 = a0 + bf16_to_f32((uint16_t)v.x) * w[k];
-      a1 = a1 + bf16_to_f32((uint16_t)(v.x >> 16)) * w[k];
-      a2 = a2 + bf16_to_f32((uint16_t)v.y) * w[k];
-      a3 = a3 + bf16_to_f32((uint16_t)(v.y >> 16)) * w[k];
+  for (int k = 0; k < kTopK; ++k) {
+    const uint4* src = (const uint4*)(down + (size_t)max(row[k], 0) * kH + c);
+    if (row[k] >= 0) {
+      v[k][0] = src[0];
+      v[k][1] = src[1];
     }
-    uint2 packed;
-    packed.x = (uint32_t)f32_to_bf16_rne(a0) | ((uint32_t)f32_to_bf16_rne(a1) << 16);
-    packed.y = (uint32_t)f32_to_bf16_rne(a2) | ((uint32_t)f32_to_bf16_rne(a3) << 16);
-    *(uint2*)(out + (size_t)t * kH + c) = packed;
   }
+  float a[kCombCols];
+#pragma unroll
+  for (int i = 0; i < kCombCols; ++i) a[i] = 0.f;
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) {
+    if (row[k] < 0) continue;  // token-uniform
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t u[4] = {v[k][h].x, v[k][h].y, v[k][h].z, v[k][h].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        a[8 * h + 2 * q] = a[8 * h + 2 * q] + bf16_to_f32((uint16_t)u[q]) * w[k];
+        a[8 * h + 2 * q + 1] = a[8 * h + 2 * q + 1] + bf16_to_f32((uint16_t)(u[q] >> 16)) * w[k];
+      }
+    }
+  }
+  uint4 o[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint32_t p[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      p[q] = (uint32_t)f32_to_bf16_rne(a[8 * h + 2 * q]) | ((uint32_t)f32_to_bf16_rne(a[8 * h + 2 * q + 1]) << 16);
+    o[h] = uint4{p[0], p[1], p[2], p[3]};
+  }
+  uint4* dst = (uint4*)(out + (size_t)t * kH + c);
+  dst[0] = o[0];
+  dst[1] = o[1];
 }
 
 }  // namespace
