@@ -69,7 +69,10 @@ inline Layout make_layout(int64_t T) {
 //     half the L2 -> LDS rate;
 //   * chunk c of row r land at slot c ^ swz(r), so that the MFMA operand
 //     reads, where the 16 lanes of a quarter read 16 rows at the same logical
-//     chunk, fall on 16 distinct 16-byte bank groups.
+//     chunk, fall on distinct 16-byte bank groups both within every 8 lanes
+//     (128 bytes of banks) and within all 16 (256 bytes).  The narrow
+//     swizzle (r/4 ^ r/2) is the one that satisfies both: r/4 alone left
+//     GEMM2's B reads with bank conflicts on a third of the LDS cycles.
 // MFMA lane (q = lane / 16, r = lane % 16) reads row r at logical chunks
 //   * wide: 2q and 2q + 1 (K bytes 32q .. 32q+31 of the row);
 //   * narrow: q (K bytes 16q .. 16q+15).
@@ -77,7 +80,7 @@ inline Layout make_layout(int64_t T) {
 // the bf16 activation rows are stored in natural column order.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int swz_wide(int r) { return (r & 7) ^ (r >> 3); }  // r < 16
-__device__ __forceinline__ int swz_narrow(int r) { return (r >> 2) & 3; }      // r < 16
+__device__ __forceinline__ int swz_narrow(int r) { return ((r >> 2) ^ (r >> 1)) & 3; }  // r < 16
 
 // Copy lane -> (row of the fragment, source chunk) for wide plane `half`.
 __device__ __forceinline__ void wide_copy_lane(int lane, int half, int& row, int& chunk) {
