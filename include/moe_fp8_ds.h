@@ -120,6 +120,17 @@ typedef struct {
 
 int moe_fp8_ds_workspace_layout(int64_t T, moe_fp8_ds_layout* layout);
 
+/* The step before the layer.  No counterpart in the reference, which only
+ * consumes its result: hidden_states [T,7168] e4m3 and hidden_states_scale
+ * [56,T] fp32 (moe.py:32-33, moe.cu:2650-2661).  Quantises bf16 hidden rows
+ * [T,7168] per 128-column block: scale = absmax/448 (1 for an all-zero
+ * block; NaN does not enter the absmax), q = e4m3(x/scale) rounded to nearest
+ * even and saturated to +-448; scales are written transposed, [56,T].
+ * hidden_bf16 must be 16-byte aligned, hidden_fp8 8-byte aligned.  Stream
+ * ordered, no allocation, T == 0 is a no-op. */
+int moe_fp8_ds_quantize_hidden(const void* hidden_bf16, int64_t T, void* hidden_fp8, float* hidden_scale,
+                               hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,6 +10,6 @@ so import it with importlib:
     pkg.run(...)
 """
 from . import _lib, synth  # noqa: F401
-from .moe import intermediates, route, run, workspace  # noqa: F401
+from .moe import intermediates, quantize_hidden, route, run, workspace  # noqa: F401
 
-__all__ = ["run", "route", "intermediates", "workspace", "synth"]
+__all__ = ["run", "route", "intermediates", "workspace", "quantize_hidden", "synth"]

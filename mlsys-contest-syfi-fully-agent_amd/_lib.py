@@ -51,6 +51,8 @@ def moe_lib() -> ctypes.CDLL:
         L.moe_fp8_ds_run_profiled.restype = ctypes.c_int
         L.moe_fp8_ds_route.argtypes = [P, P, i64, dbl, i64, P, sz, P]
         L.moe_fp8_ds_route.restype = ctypes.c_int
+        L.moe_fp8_ds_quantize_hidden.argtypes = [P, i64, P, P, P]
+        L.moe_fp8_ds_quantize_hidden.restype = ctypes.c_int
         _moe = L
     return _moe
 

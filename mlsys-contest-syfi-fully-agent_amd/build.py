@@ -38,7 +38,7 @@ FLAGS = [
 ]
 
 LIBS = {
-    "libmoe_fp8_ds.so": ["route.hip", "gemm1.hip", "gemm2.hip", "combine.hip", "moe_api.cpp"],
+    "libmoe_fp8_ds.so": ["route.hip", "gemm1.hip", "gemm2.hip", "combine.hip", "quantize.hip", "moe_api.cpp"],
     "libmoe_synth.so": ["synth.hip"],
 }
 

@@ -15,5 +15,7 @@ bool gemm2_fuses_combine(int T);
 hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws, void* out,
                         hipStream_t stream);
 hipError_t launch_combine(int T, const Layout& L, char* ws, void* out, hipStream_t stream);
+// bf16 hidden rows -> e4m3 rows + transposed per-128-block scales.
+hipError_t launch_quantize_hidden(const uint16_t* x, int T, uint8_t* q, float* scale, hipStream_t stream);
 
 }  // namespace moe

@@ -106,6 +106,34 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_
     return output
 
 
+def quantize_hidden(hidden_states, hidden_states_fp8=None, hidden_states_scale=None):
+    """The step before the layer: bf16 hidden rows [T, 7168] -> the layer's
+    `hidden_states` (e4m3, [T, 7168]) and `hidden_states_scale` (fp32, [56, T],
+    transposed), one scale per 128 columns: absmax/448 (1 for an all-zero
+    block), values rounded to nearest even and saturated to +-448
+    (moe_fp8_ds_quantize_hidden).  Outputs are allocated unless given; the
+    work is enqueued on the current stream."""
+    assert hidden_states.dtype == torch.bfloat16 and hidden_states.dim() == 2 and hidden_states.shape[1] == H
+    assert hidden_states.is_contiguous()
+    dev = hidden_states.device
+    if dev.type != "cuda":
+        raise RuntimeError("moe_fp8_ds runs on a ROCm GPU only (no CPU path)")
+    T = hidden_states.shape[0]
+    if hidden_states_fp8 is None:
+        hidden_states_fp8 = torch.empty((T, H), dtype=torch.float8_e4m3fn, device=dev)
+    if hidden_states_scale is None:
+        hidden_states_scale = torch.empty((H // BLOCK, T), dtype=torch.float32, device=dev)
+    assert hidden_states_fp8.dtype == torch.float8_e4m3fn and hidden_states_fp8.shape == (T, H)
+    assert hidden_states_scale.dtype == torch.float32 and hidden_states_scale.shape == (H // BLOCK, T)
+    assert hidden_states_fp8.is_contiguous() and hidden_states_scale.is_contiguous()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    rc = _lib.moe_lib().moe_fp8_ds_quantize_hidden(_ptr(hidden_states), T, _ptr(hidden_states_fp8),
+                                                   _ptr(hidden_states_scale), stream)
+    if rc != _lib.OK:
+        raise RuntimeError(f"moe_fp8_ds_quantize_hidden: {_lib.status_string(rc)} ({rc})")
+    return hidden_states_fp8, hidden_states_scale
+
+
 class RouteResult:
     """Typed views of the routing/permutation regions of a workspace."""
 

@@ -65,6 +65,14 @@ void synth_w13(uint64_t seed, int e0, int e1, uint8_t* q, float* scale);
 /* gemm2 weights [32,7168,2048] e4m3 + scales [32,56,16]; experts [e0,e1). */
 void synth_w2(uint64_t seed, int e0, int e1, uint8_t* q, float* scale);
 
+/* ---- activation quantiser (the step before the layer) ------------------ */
+/* bf16 hidden rows [T,7168] -> e4m3 [T,7168] + transposed scales [56,T]:
+ * scale = absmax/448 over the block's non-NaN |x| (1 if that is 0),
+ * q = orc_f32_to_e4m3(x / scale).  The convention of synth_hidden, applied
+ * to given values.  No counterpart in the reference (it consumes the result,
+ * moe.py:32-33). */
+void orc_quantize_hidden(const uint16_t* x, int64_t T, uint8_t* q, float* scale);
+
 /* ---- routing (moe.py:123-158) ---------------------------------------- */
 /* For each token: the 8 selected global expert ids sorted ascending, their
  * combination weights, and (optional) the fp32 sigmoid / biased scores.

@@ -50,6 +50,7 @@ def lib() -> ctypes.CDLL:
         L.synth_w13.argtypes = [u64, i32, i32, P, P]
         L.synth_w2.argtypes = [u64, i32, i32, P, P]
         L.orc_route.argtypes = [P, P, i64, f32, P, P, P, P]
+        L.orc_quantize_hidden.argtypes = [P, i64, P, P]
         L.orc_moe.argtypes = [P, P, P, P, P, P, P, P, i64, f32, i64, P, i64, P, i32]
         L.orc_moe.restype = i32
         L.orc_expert_rows.argtypes = [P, P, i64, P, P, P, P, P, P, i64, P, P]
@@ -189,3 +190,14 @@ def bf16_to_f32(u16: np.ndarray) -> np.ndarray:
 def e4m3_to_f32(u8: np.ndarray) -> np.ndarray:
     lut = np.array([lib().orc_e4m3_to_f32(i) for i in range(256)], np.float32)
     return lut[u8]
+
+
+def quantize_hidden(x_bf16: np.ndarray):
+    """bf16 bits [T, 7168] (uint16) -> (e4m3 bits uint8 [T, 7168], scales f32 [56, T])."""
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    T = x.shape[0]
+    q = np.empty((T, H), dtype=np.uint8)
+    sc = np.empty((H // 128, T), dtype=np.float32)
+    lib().orc_quantize_hidden(_p(x), T, _p(q), _p(sc))
+    return q, sc
+

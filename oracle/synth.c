@@ -163,6 +163,24 @@ void synth_hidden(uint64_t seed, int64_t T, uint8_t* q, float* scale) {
   }
 }
 
+void orc_quantize_hidden(const uint16_t* x, int64_t T, uint8_t* q, float* scale) {
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < T; ++t) {
+    for (int b = 0; b < ORC_NH_BLK; ++b) {
+      const uint16_t* src = x + t * ORC_H + b * ORC_BLOCK;
+      float amax = 0.0f;
+      for (int j = 0; j < ORC_BLOCK; ++j) {
+        const float a = fabsf(orc_bf16_to_f32(src[j]));
+        if (a > amax) amax = a; /* NaN never compares greater */
+      }
+      const float s = block_scale(amax);
+      scale[(int64_t)b * T + t] = s;
+      uint8_t* dst = q + t * ORC_H + b * ORC_BLOCK;
+      for (int j = 0; j < ORC_BLOCK; ++j) dst[j] = orc_f32_to_e4m3(orc_bf16_to_f32(src[j]) / s);
+    }
+  }
+}
+
 /* Generic [E, R, C] weight with 128x128 block scales [E, R/128, C/128]. */
 static void synth_weight(uint64_t seed, uint32_t stream, float sigma, int rows, int cols, int e0,
                          int e1, uint8_t* q, float* scale) {

@@ -99,3 +99,18 @@ def test_python_entry_rejects_bad_shapes(pkg):
             torch.zeros(1)]
     with pytest.raises(AssertionError):
         pkg.run(*args, 0, 2.5, torch.zeros(T, 7168, dtype=torch.bfloat16))
+
+
+def test_quantize_validation_without_gpu(pkg):
+    L = pkg._lib.moe_lib()
+    buf = ctypes.create_string_buffer(64 + 256)
+    base = ctypes.addressof(buf)
+    al = base + (-base) % 256  # never dereferenced: every case returns before a launch
+    assert L.moe_fp8_ds_quantize_hidden(al, 0, al, al, None) == 0  # T == 0: no-op
+    assert L.moe_fp8_ds_quantize_hidden(al, -1, al, al, None) == -2
+    assert L.moe_fp8_ds_quantize_hidden(al, L.moe_fp8_ds_max_tokens() + 1, al, al, None) == -2
+    assert L.moe_fp8_ds_quantize_hidden(None, 4, al, al, None) == -1
+    assert L.moe_fp8_ds_quantize_hidden(al, 4, al, None, None) == -1
+    assert L.moe_fp8_ds_quantize_hidden(al + 8, 4, al, al, None) == -3   # bf16 rows need 16 B
+    assert L.moe_fp8_ds_quantize_hidden(al, 4, al + 4, al, None) == -3   # e4m3 rows need 8 B
+    assert L.moe_fp8_ds_quantize_hidden(al, 4, al, al + 2, None) == -3   # scales need 4 B
