@@ -242,6 +242,44 @@ def cpu_baseline(pkg, torch, wl, budget_tokens):
     }
 
 
+def measure_quantizer(pkg, torch, dev, T, iters=100):
+    """The step before the layer (pkg.quantize_hidden): bf16 rows [T, 7168]
+    -> e4m3 rows + [56, T] scales.  HBM-bound; algorithmic bytes per call =
+    T * (2 * 7168 read + 7168 + 56 * 4 written).  Inputs rotate over enough
+    buffers (>= 1 GiB together) that each call reads its rows from HBM, not
+    from the 256 MB MALL."""
+    copies = max(4, (1 << 30) // (T * H * 2) + 1)
+    g = torch.Generator(device="cpu").manual_seed(T)
+    base = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    xs = [base.roll(i, 0).contiguous() for i in range(copies)]
+    q = torch.empty(T, H, dtype=torch.float8_e4m3fn, device=dev)
+    sc = torch.empty(H // 128, T, dtype=torch.float32, device=dev)
+    for i in range(3):
+        pkg.quantize_hidden(xs[i % copies], q, sc)
+    torch.cuda.synchronize()
+    # The launches are captured in a graph and replayed, so the events time the
+    # kernels back to back rather than the Python wrapper's launch rate (a
+    # T = 1024 kernel is shorter than one pass through the wrapper).
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(iters):
+            pkg.quantize_hidden(xs[i % copies], q, sc)
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) / iters * 1e3
+    del graph
+    nbytes = T * (2 * H + H + (H // 128) * 4)
+    return {"T": T, "latency_us": round(us, 3), "gbps": round(nbytes / us / 1e3, 1),
+            "roofline": {"bound": "hbm", "achieved": round(nbytes / us / 1e3, 1), "peak": HBM_PEAK / 1e9,
+                         "unit": "GB/s", "frac": round(nbytes / us / 1e3 / (HBM_PEAK / 1e9), 4)},
+            "algo_bytes": nbytes}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -254,6 +292,7 @@ def main():
     ap.add_argument("--trials", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-tokens", type=int, default=1024)
+    ap.add_argument("--no-quant", action="store_true", help="skip the activation-quantiser measurement")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this size (for PMC byte calibration)")
     args = ap.parse_args()
@@ -288,6 +327,12 @@ def main():
 
     if args.copy_calib_mib:
         copy_calibration(torch, dev, args.copy_calib_mib)
+    quant = {}
+    if not args.no_quant:
+        for Tq in (1024, 8192):
+            quant[f"t{Tq}"] = measure_quantizer(pkg, torch, dev, Tq)
+            log(f"[bench] quantize_hidden T={Tq}: {quant[f't{Tq}']['latency_us']:.1f} us "
+                f"{quant[f't{Tq}']['gbps']:.0f} GB/s")
 
     dom = hm["dominant"]
     roof = {"bound": dom["bound"], "achieved": round(dom["achieved"], 3), "peak": dom["peak"],
@@ -307,6 +352,7 @@ def main():
         "tflops": round(hm["tflops"], 2), "gbps": round(hm["gbps"], 1), "layer_roofline_frac": round(hm["roofline_frac"], 4),
         "roofline": roof,
         "cpu_baseline": cpu,
+        "upstream_quantizer": quant or None,
         "per_workload": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                          for k, v in results.items()},
     }

@@ -216,6 +216,28 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0_rt(int n) {
   }
 }
 
+// ---- DPP helpers (GFX9 controls) -------------------------------------------
+constexpr int kDppQuad1032 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kDppQuad2301 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowBcast15 = 0x142;
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  // lanes outside ROW_MASK keep their own value (old = v)
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Maximum of a 32-bit value over each row of 16 lanes, in every lane of the row.
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t k) {
+  k = max(k, dpp_u32<kDppQuad1032, 0xF>(k));
+  k = max(k, dpp_u32<kDppQuad2301, 0xF>(k));
+  k = max(k, dpp_u32<kDppRowHalfMirror, 0xF>(k));
+  k = max(k, dpp_u32<kDppRowMirror, 0xF>(k));
+  return k;
+}
+
 // Workgroup barrier that the compiler may not move memory accesses across.
 __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");

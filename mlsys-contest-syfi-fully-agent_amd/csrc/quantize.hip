@@ -7,44 +7,115 @@
 //   q     = e4m3(x / scale), round to nearest even, saturating to +-448
 // NaN elements do not enter the absmax and encode as NaN.
 //
-// Design (gfx950): HBM-bound (reads 2 B and writes 1 B per element).  One
-// wave per token row; each pass of a wave covers 512 columns = 4 scale blocks
-// with 16 lanes per block, every lane loading 16 contiguous bytes (8 bf16).
-// A block's absmax is a 16-lane max; the wave's scales go through LDS so that
-// the transposed scale rows are written as 16 contiguous tokens.
+// Design (gfx950): HBM-bound (reads 2 B and writes 1 B per element), so the
+// arithmetic per element has to stay under the memory time.  One wave per
+// token row, four rows per workgroup (T/4 workgroups: 256 at T = 1024).  A
+// wave issues all 14 row loads (16 B per lane each) before any arithmetic, so
+// a token has its whole 14 KB row in flight at once; each of the 7 passes
+// then covers 1024 columns = 8 scale blocks, 8 lanes per block and 16
+// contiguous elements per lane.  A block's absmax is an 8-lane DPP max of
+// bf16 magnitudes (compared as integers); the scales go through LDS so that
+// each transposed scale row is written as 4 contiguous tokens.
+//
+// Fast path (every pass whose blocks all have 2^-96 <= absmax < inf or
+// absmax = 0, and no NaN): with s = absmax / 448 and r = 1 / s (both
+// correctly rounded),
+//   q = x * r;  q' = fma(fma(-s, q, x), r, q);  code = e4m3_rne(|q'|) | sign(x)
+// and the rounding to e4m3 is v_cvt_pk_fp8_f32.  Both steps were checked
+// exhaustively against the correctly rounded x / s followed by the software
+// RNE conversion below: q' gives the same e4m3 code for every bf16 pair
+// |x| <= absmax in that range (about 1.07e9 pairs), and the hardware
+// conversion equals the software one for every fp32 with |y| < 464 (|q'| is
+// at most 448 * (1 + 2^-22)).  Passes with a NaN, an infinity or a tiny
+// absmax in any of the wave's blocks take the exact path (IEEE division and
+// the software conversion) instead; that branch is wave-uniform.
 #include "kernels.hpp"
 
 namespace moe {
 namespace {
 
-constexpr int kQTokens = 16;  // tokens (waves) per workgroup
+constexpr int kQTokens = 4;   // tokens (waves) per workgroup
 constexpr int kQThreads = kQTokens * kWave;
-constexpr int kQPass = 512;   // columns per wave pass
+constexpr int kQLaneCols = 16;                 // elements per lane per pass
+constexpr int kQPass = kWave * kQLaneCols;     // 1024 columns per wave pass
+constexpr int kQPasses = kH / kQPass;          // 7
+constexpr int kQLanesPerBlk = kBlk / kQLaneCols;  // 8
+constexpr uint32_t kQTinyBf16 = 0x0F80u;       // bf16 bits of 2^-96
 
-// fp32 -> OCP e4m3fn, round to nearest even, saturating finite values;
-// NaN -> 0x7F (sign kept).
+// fp32 -> OCP e4m3fn, round to nearest even, saturating finite values and
+// infinities to +-448; NaN -> 0x7F (sign kept).  Branch-free:
+//   normal range (|x| >= 2^-6): adding 2^19 - 1 + (bit 20) to the magnitude's
+//     bits rounds its 23-bit mantissa to 3 bits, nearest even, with the carry
+//     running into the exponent; the code is then (bits >> 20) - (120 << 3)
+//     (exponent rebias 127 -> 7), clamped to 0x7E (448);
+//   subnormal range: the code is |x| / 2^-9 rounded to nearest even (0..8,
+//     8 being the smallest normal, 0x08).
 __device__ __forceinline__ uint32_t f32_to_e4m3_satfinite(float x) {
   const uint32_t u = __float_as_uint(x);
   const uint32_t sign = (u >> 24) & 0x80u;
   const uint32_t a = u & 0x7FFFFFFFu;
-  if (a > 0x7F800000u) return sign | 0x7Fu;
-  const float af = __uint_as_float(a);
-  if (af >= 448.0f) return sign | 0x7Eu;
-  if (af < 0x1p-6f) return sign | (uint32_t)rintf(af * 512.0f);  // subnormal grid 2^-9, RNE
-  int e = (int)(a >> 23) - 127;
-  uint32_t keep = (a >> 20) & 7u;
-  const uint32_t rem = a & 0xFFFFFu;
-  if (rem > 0x80000u || (rem == 0x80000u && (keep & 1u))) {
-    if (++keep == 8u) {
-      keep = 0;
-      ++e;
-    }
-  }
-  if (e > 8 || (e == 8 && keep == 7u)) return sign | 0x7Eu;
-  return sign | ((uint32_t)(e + 7) << 3) | keep;
+  const uint32_t normal = min(((a + 0x7FFFFu + ((a >> 20) & 1u)) >> 20) - 960u, 0x7Eu);
+  const uint32_t sub = (uint32_t)rintf(__uint_as_float(a) * 512.0f);
+  uint32_t code = a < 0x3C800000u ? sub : normal;
+  code = a > 0x7F800000u ? 0x7Fu : code;
+  return sign | code;
 }
 
-__device__ __forceinline__ float fmax_nonnan(float a, float b) { return b > a ? b : a; }
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
+
+// Largest bf16 magnitude (as bits, 0..0x7FFF) of the 16 elements of one lane;
+// NaN patterns (> 0x7F80) order above every number, so a NaN shows as > 0x7F80.
+__device__ __forceinline__ uint32_t lane_absmax_bits(const uint4& a, const uint4& b) {
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    lo = max(lo, w[i] & 0x7FFFu);
+    hi = max(hi, (w[i] >> 16) & 0x7FFFu);
+  }
+  return max(lo, hi);
+}
+
+// The same with NaN elements left out (the exact path's absmax).
+__device__ __forceinline__ uint32_t lane_absmax_bits_nonnan(const uint4& a, const uint4& b) {
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t lo = w[i] & 0x7FFFu, hi = (w[i] >> 16) & 0x7FFFu;
+    m = max(m, lo > 0x7F80u ? 0u : lo);
+    m = max(m, hi > 0x7F80u ? 0u : hi);
+  }
+  return m;
+}
+
+// Maximum over each group of 8 lanes (a scale block), in every lane of it.
+__device__ __forceinline__ uint32_t group8_max_u32(uint32_t k) {
+  k = max(k, dpp_u32<kDppQuad1032, 0xF>(k));
+  k = max(k, dpp_u32<kDppQuad2301, 0xF>(k));
+  return max(k, dpp_u32<kDppRowHalfMirror, 0xF>(k));
+}
+
+// Four elements (signs from the inputs) -> four e4m3 bytes, fast path.
+__device__ __forceinline__ uint32_t fast_pack4(float x0, float x1, float x2, float x3, float s, float r) {
+  const float x[4] = {x0, x1, x2, x3};
+  float y[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float q = x[i] * r;
+    const float q2 = fmaf(fmaf(-s, q, x[i]), r, q);
+    y[i] = __uint_as_float((__float_as_uint(q2) & 0x7FFFFFFFu) | (__float_as_uint(x[i]) & 0x80000000u));
+  }
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], lo, true);
+}
+
+// The same, exact path: IEEE division and the software conversion.
+__device__ __forceinline__ uint32_t exact_pack4(float x0, float x1, float x2, float x3, float s) {
+  return f32_to_e4m3_satfinite(x0 / s) | (f32_to_e4m3_satfinite(x1 / s) << 8) |
+         (f32_to_e4m3_satfinite(x2 / s) << 16) | (f32_to_e4m3_satfinite(x3 / s) << 24);
+}
 
 __global__ void __launch_bounds__(kQThreads)
 quantize_hidden_kernel(const uint16_t* __restrict__ x, int T, uint8_t* __restrict__ q,
@@ -54,38 +125,45 @@ quantize_hidden_kernel(const uint16_t* __restrict__ x, int T, uint8_t* __restric
   const int lane = threadIdx.x & (kWave - 1);
   const int t = blockIdx.x * kQTokens + w;
   if (t < T) {
-    const uint16_t* row = x + (size_t)t * kH;
-    uint8_t* qrow = q + (size_t)t * kH;
-#pragma unroll 2
-    for (int c = 0; c < kH / kQPass; ++c) {
-      const int col = c * kQPass + lane * 8;
-      const uint4 raw = *(const uint4*)(row + col);
-      const uint32_t u[4] = {raw.x, raw.y, raw.z, raw.w};
-      float v[8];
+    const uint16_t* row = x + (size_t)t * kH + lane * kQLaneCols;
+    uint8_t* qrow = q + (size_t)t * kH + lane * kQLaneCols;
+    // the whole row (14 x 16 B per lane) is in flight before any arithmetic
+    uint4 raw[2 * kQPasses];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[2 * i] = __uint_as_float(u[i] << 16);
-        v[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+    for (int c = 0; c < kQPasses; ++c) {
+      raw[2 * c] = *(const uint4*)(row + c * kQPass);
+      raw[2 * c + 1] = *(const uint4*)(row + c * kQPass + 8);
+    }
+#pragma unroll
+    for (int c = 0; c < kQPasses; ++c) {
+      const uint4 a = raw[2 * c], b = raw[2 * c + 1];
+      const uint32_t m = group8_max_u32(lane_absmax_bits(a, b));
+      const bool odd = m > 0x7F7Fu || (m != 0u && m < kQTinyBf16);
+      const uint32_t e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      uint4 out;
+      float s;
+      if (__ballot(odd) == 0) {
+        const float amax = __uint_as_float(m << 16);
+        s = amax > 0.0f ? amax / 448.0f : 1.0f;
+        const float r = 1.0f / s;
+        out.x = fast_pack4(bf16_lo(e[0]), bf16_hi(e[0]), bf16_lo(e[1]), bf16_hi(e[1]), s, r);
+        out.y = fast_pack4(bf16_lo(e[2]), bf16_hi(e[2]), bf16_lo(e[3]), bf16_hi(e[3]), s, r);
+        out.z = fast_pack4(bf16_lo(e[4]), bf16_hi(e[4]), bf16_lo(e[5]), bf16_hi(e[5]), s, r);
+        out.w = fast_pack4(bf16_lo(e[6]), bf16_hi(e[6]), bf16_lo(e[7]), bf16_hi(e[7]), s, r);
+      } else {
+        const float amax = __uint_as_float(group8_max_u32(lane_absmax_bits_nonnan(a, b)) << 16);
+        s = amax > 0.0f ? amax / 448.0f : 1.0f;
+        out.x = exact_pack4(bf16_lo(e[0]), bf16_hi(e[0]), bf16_lo(e[1]), bf16_hi(e[1]), s);
+        out.y = exact_pack4(bf16_lo(e[2]), bf16_hi(e[2]), bf16_lo(e[3]), bf16_hi(e[3]), s);
+        out.z = exact_pack4(bf16_lo(e[4]), bf16_hi(e[4]), bf16_lo(e[5]), bf16_hi(e[5]), s);
+        out.w = exact_pack4(bf16_lo(e[6]), bf16_hi(e[6]), bf16_lo(e[7]), bf16_hi(e[7]), s);
       }
-      float amax = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmax_nonnan(amax, fabsf(v[i]));
-      // max over the 16 lanes of this block (xor 1, 2, 4, 8 stay inside it)
-#pragma unroll
-      for (int m = 1; m < 16; m <<= 1) amax = fmax_nonnan(amax, __shfl_xor(amax, m, kWave));
-      const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lo |= f32_to_e4m3_satfinite(v[i] / s) << (8 * i);
-        hi |= f32_to_e4m3_satfinite(v[4 + i] / s) << (8 * i);
-      }
-      *(uint2*)(qrow + col) = uint2{lo, hi};
-      if ((lane & 15) == 0) sc[c * 4 + (lane >> 4)][w] = s;
+      *(uint4*)(qrow + c * kQPass) = out;
+      if ((lane & (kQLanesPerBlk - 1)) == 0) sc[c * (kQPass / kBlk) + lane / kQLanesPerBlk][w] = s;
     }
   }
   __syncthreads();
-  // scale[b][t0 .. t0+15]: 16 contiguous floats per block row
+  // scale[b][t0 .. t0+kQTokens-1]: contiguous floats per block row
   const int t0 = blockIdx.x * kQTokens;
   for (int i = threadIdx.x; i < kNHBlk * kQTokens; i += kQThreads) {
     const int b = i / kQTokens, k = i % kQTokens;

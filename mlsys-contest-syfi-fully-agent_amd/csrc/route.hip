@@ -32,26 +32,10 @@ namespace {
 constexpr int kRouteWaves = 16;
 constexpr int kRouteThreads = kRouteWaves * kWave;
 
-// ---- DPP helpers (GFX9 controls) -------------------------------------------
-constexpr int kDppQuad1032 = 0xB1;    // quad_perm [1,0,3,2]
-constexpr int kDppQuad2301 = 0x4E;    // quad_perm [2,3,0,1]
-constexpr int kDppRowHalfMirror = 0x141;
-constexpr int kDppRowMirror = 0x140;
-constexpr int kDppRowBcast15 = 0x142;
-
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  // lanes outside ROW_MASK keep their own value (old = v)
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROW_MASK, 0xF, false);
-}
-
 // Maxima of the two half-waves (lanes 0-31, 32-63) of a 32-bit key,
 // wave-uniform.  Four DPP row steps, then rows 1 and 3 take rows 0 and 2.
 __device__ __forceinline__ void halfwave_max(uint32_t k, uint32_t& m0, uint32_t& m1) {
-  k = max(k, dpp_u32<kDppQuad1032, 0xF>(k));
-  k = max(k, dpp_u32<kDppQuad2301, 0xF>(k));
-  k = max(k, dpp_u32<kDppRowHalfMirror, 0xF>(k));
-  k = max(k, dpp_u32<kDppRowMirror, 0xF>(k));
+  k = row16_max_u32(k);
   k = max(k, dpp_u32<kDppRowBcast15, 0xA>(k));
   m0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 31);
   m1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 63);

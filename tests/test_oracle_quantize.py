@@ -87,3 +87,50 @@ def test_rows_are_independent(orc, T):
     q1, sc1 = orc.quantize_hidden(x[-1:])
     np.testing.assert_array_equal(q[-1:], q1)
     np.testing.assert_array_equal(sc[:, -1:], sc1)
+
+
+# ---- the GPU kernel's fast arithmetic, checked exhaustively on the CPU ------
+# tests/support/quant_fastpath.c restates the kernel's fast quotient
+# (q = x*r, q' = fma(fma(-s, q, x), r, q), sign from x) with the same single
+# IEEE fp32 operations and compares its e4m3 code with the oracle's correctly
+# rounded x / s for every bf16 pair |x| <= absmax.
+
+def _fastpath_lib():
+    import ctypes
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "support", "_build", "libquant_fastpath.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+    L = ctypes.CDLL(path)
+    L.quant_fastpath_mismatches.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int,
+                                            ctypes.POINTER(ctypes.c_uint64)]
+    L.quant_fastpath_mismatches.restype = ctypes.c_uint64
+    return L
+
+
+def _mismatches(L, lo, hi, variant):
+    import ctypes
+
+    pairs = ctypes.c_uint64(0)
+    bad = L.quant_fastpath_mismatches(lo, hi, variant, ctypes.byref(pairs))
+    return int(bad), int(pairs.value)
+
+
+def test_fast_quotient_exhaustive():
+    """Every block maximum the kernel's fast path accepts (0, or 2^-96 <= amax
+    < inf; bf16 bits 0 and 0x0F80..0x7F7F) and every bf16 |x| <= amax."""
+    L = _fastpath_lib()
+    bad, pairs = _mismatches(L, 0x0F80, 0x7F80, 0)
+    assert pairs > 1_000_000_000
+    assert bad == 0
+    assert _mismatches(L, 0, 1, 0) == (0, 2)  # amax = 0: x = +-0
+
+
+def test_fast_quotient_check_has_teeth():
+    """Planted mistakes fail the same check: no correction step, no sign fix,
+    and tiny block maxima (< 2^-96, which the kernel sends to its exact path)."""
+    L = _fastpath_lib()
+    assert _mismatches(L, 0x3F00, 0x3F80, 1)[0] > 0   # y = x * r
+    assert _mismatches(L, 0x3F00, 0x3F80, 2)[0] > 0   # -0 loses its sign
+    assert _mismatches(L, 0x0400, 0x0F80, 0)[0] > 0   # below the fast path's range
