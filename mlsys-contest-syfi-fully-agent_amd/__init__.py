@@ -9,7 +9,7 @@ so import it with importlib:
     pkg = importlib.import_module("mlsys-contest-syfi-fully-agent_amd")
     pkg.run(...)
 """
-from . import _lib, synth  # noqa: F401
+from . import _lib, synth, verdict, workloads  # noqa: F401
 from .moe import intermediates, quantize_hidden, route, run, workspace  # noqa: F401
 
-__all__ = ["run", "route", "intermediates", "workspace", "quantize_hidden", "synth"]
+__all__ = ["run", "route", "intermediates", "workspace", "quantize_hidden", "synth", "workloads", "verdict"]
