@@ -48,122 +48,215 @@ constexpr int kS1Threads = kS1Waves * kWave;
 constexpr int kS1KB = kNHBlk / kS1Waves;  // 7 scale blocks per wave
 constexpr int kS1Groups = kI / 8;         // 256 column groups per expert
 
+// Operands of one 16-row tile that go out before it is multiplied.
+struct S1TileOps {
+  v8i a[kS1KB];     // A rows (token rows of hidden_states), this wave's K range
+  float s0, s1;     // two of the tile's activation scale entries (lane l: l and 64 + l)
+  float sw[kS1KB];  // weight block scales of this lane's column
+  int ptok;         // kDirect: token of the expert's permuted row threadIdx.x (< M)
+};
+
+// SwiGLU output of one tile held by each of waves 0-3 (its rows 4q + wave)
+// until the next item's loads are out (a store issued before them would
+// delay the wait for them).
+struct S1Out {
+  uint16_t v;
+  int row;  // destination act row, -1: none
+};
+
 template <bool kDirect>
 __global__ void __launch_bounds__(kS1Threads)
 gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
                     const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                     const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
                     uint16_t* __restrict__ act) {
-  __shared__ float sa[kS1Waves][kS1KB][16];   // activation scales, per wave
-  __shared__ float red[kS1Waves][4][kWave];   // K-partials
-  __shared__ int inv[16];                     // kDirect: token -> permuted row, -1 if none
+  // Per wave: the weights of the item being started (copy j of lane l at
+  // 1024 j + 16 l; the only LDS DMA target), the activation scales and the
+  // K-partials.  The permutation (<= 8 * 64 rows) is cached whole.
+  // One LDS object: with a second __shared__ array the compiler waits for
+  // every outstanding LDS DMA before any LDS read.
+  constexpr int kWBytes = 2 * kS1KB * 1024;
+  constexpr int kSaOff = kS1Waves * kWBytes;
+  constexpr int kRedOff = kSaOff + kS1Waves * kS1KB * 16 * 4;
+  constexpr int kInvOff = kRedOff + kS1Waves * 4 * kWave * 4;
+  constexpr int kPermOff = kInvOff + 16 * 4;
+  constexpr int kLdsBytes = kPermOff + kTopK * kGemm1StreamMaxTokens * 4;
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  float* red = (float*)(lds + kRedOff);
+  int* inv = (int*)(lds + kInvOff);                  // kDirect: token -> permuted row, -1 if none
+  int* perm_lds = (int*)(lds + kPermOff);
   ExpertRows X;
   X.load(expert_off);
-  const int cg = blockIdx.x % kS1Groups;
-  const int e = X.nth_active(blockIdx.x / kS1Groups);
-  if (e < 0) return;
-  const int row0 = X.begin(e);
-  const int M = X.end(e) - row0;
-
+  const uint32_t active = X.active();
+  const int items = __popc(active) * kS1Groups;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x & (kWave - 1);
   const int lq = lane >> 4;
   const int lr = lane & 15;
   const int kb0 = wave * kS1KB;
-  const int n = lr < 8 ? 8 * cg + lr : kI + 8 * cg + (lr - 8);
   // scale entries of this wave: entry x = (kb0 + x / 16, row x % 16), x < 112;
   // lane l copies entries l and 64 + l
   const int x1 = kWave + lane;
-
-  // kDirect: token of each permuted row of the expert (loaded now, used once
-  // all operand loads are in flight)
-  int my_tok = 0;
-  if (kDirect) {
-    if (threadIdx.x < 16) inv[threadIdx.x] = -1;
-    __syncthreads();
-    if (threadIdx.x < M) my_tok = perm_token[row0 + threadIdx.x];
+  char* wbuf = lds + wave * kWBytes;
+  float* sa = (float*)(lds + kSaOff) + wave * kS1KB * 16;
+  if (!kDirect) {
+    const int pairs = X.end(kELocal - 1);
+    for (int i = threadIdx.x; i < pairs; i += kS1Threads) perm_lds[i] = perm_token[i];
+    lds_barrier();
   }
 
-  // Token index of this lane's A row for row tile rt (kDirect: the token is
-  // the row itself).  Lanes of one row share it; so do the scale entries a
-  // lane copies (entries l and 64 + l both have row l % 16).
-  auto tile_token = [&](int rt) {
-    const int rows = kDirect ? T : min(16, M - rt * 16);
-    return kDirect ? min(lr, rows - 1) : perm_token[row0 + rt * 16 + min(lr, rows - 1)];
+  // W13 row of this lane for an item: gate rows 8cg.. in lanes r < 8, the
+  // matching up rows 2048 + 8cg.. in lanes r >= 8.
+  auto w_row = [&](int item) {
+    const int cg = item % kS1Groups;
+    const int e = nth_set_bit(active, item / kS1Groups);
+    return (size_t)e * k2I + (lr < 8 ? 8 * cg + lr : kI + 8 * cg + (lr - 8));
   };
-
-  v8i b[kS1KB];
-  float sw[kS1KB];
-  // One 16-row tile: scale DMA, A loads, MFMAs, K reduction, SwiGLU, store.
-  auto row_tile = [&](int rt, int tok) {
-    const int rows = kDirect ? T : min(16, M - rt * 16);
-    dma4(hs_scale + (size_t)(kb0 + (lane >> 4)) * T + tok, &sa[wave][0][0]);
-    if (x1 < kS1KB * 16) dma4(hs_scale + (size_t)(kb0 + (x1 >> 4)) * T + tok, &sa[wave][4][0]);
-    v8i a[kS1KB];
+  // An item's weights of this wave -> its LDS buffer, as 14 wide planes
+  // (K block j, rows 8h .. 8h+7 of the item's 16: gate rows 8cg.., then up
+  // rows 2048 + 8cg..), 128 bytes per row, chunks swizzled: each copy
+  // instruction reads 8 whole 128-byte row segments (the fast lane order for
+  // the vector memory path) and the fragment reads are free of bank
+  // conflicts.
+  auto copy_w = [&](int item) {
+    const int cg = item % kS1Groups;
+    const int e = nth_set_bit(active, item / kS1Groups);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int r, c;
+      wide_copy_lane(lane, h, r, c);
+      const size_t n = (size_t)e * k2I + (r < 8 ? 8 * cg + r : kI + 8 * cg + (r - 8));
+      const uint8_t* src = w13 + n * kH + kb0 * kBlk + 16 * c;
+#pragma unroll
+      for (int j = 0; j < kS1KB; ++j) dma16(src + j * kBlk, wbuf + (2 * j + h) * 1024);
+    }
+  };
+  // Row tile rt of an item: token of this lane's A row (kDirect: the rows
+  // are the tokens themselves), then the tile's row operands -- the same for
+  // every item of one expert.
+  auto issue_rows = [&](int item, int rt, S1TileOps& o) {
+    const int e = nth_set_bit(active, item / kS1Groups);
+    const int row0 = X.begin(e) + rt * 16;
+    const int rows = kDirect ? T : min(16, X.end(e) - row0);
+    const int tok = kDirect ? min(lr, rows - 1) : perm_lds[row0 + min(lr, rows - 1)];
+    o.s0 = hs_scale[(size_t)(kb0 + (lane >> 4)) * T + tok];
+    o.s1 = x1 < kS1KB * 16 ? hs_scale[(size_t)(kb0 + (x1 >> 4)) * T + tok] : 0.f;
     const uint8_t* ap = hs + (size_t)tok * kH + kb0 * kBlk + 32 * lq;
 #pragma unroll
-    for (int j = 0; j < kS1KB; ++j) a[j] = *(const v8i*)(ap + j * kBlk);
-    // Every load of this wave, the scale DMA included, has landed before the
-    // first MFMA: the empty asm pins all operand registers here, so the
-    // compiler issues every load above it and cannot interleave loads with
-    // the MFMAs (which would serialise HBM round trips).
+    for (int j = 0; j < kS1KB; ++j) o.a[j] = *(const v8i*)(ap + j * kBlk);
+    o.ptok = 0;
+    if (kDirect && (int)threadIdx.x < X.end(e) - X.begin(e)) o.ptok = perm_token[X.begin(e) + threadIdx.x];
+  };
+  // The item's weight block scales (this lane's column).
+  auto issue_sw = [&](int item, S1TileOps& o) {
+    const float* sp = w13_scale + (w_row(item) / kBlk) * kNHBlk + kb0;
 #pragma unroll
-    for (int j = 0; j < kS1KB; ++j) asm volatile("" : "+v"(a[j]), "+v"(b[j]));
-    wait_vmcnt_lgkm0<0>();
-    asm volatile("" ::: "memory");
-    if (kDirect && threadIdx.x < M) inv[my_tok] = row0 + threadIdx.x;  // read after the barrier below
+    for (int j = 0; j < kS1KB; ++j) o.sw[j] = sp[j];
+  };
+  // Multiply a landed tile, reduce the 8 K-partials in a fixed order, SwiGLU,
+  // store the activation rows.
+  auto compute_tile = [&](int item, int rt, const S1TileOps& o, const v8i (&b)[kS1KB], S1Out& out) {
+    const int cg = item % kS1Groups;
+    const int e = nth_set_bit(active, item / kS1Groups);
+    const int row0 = X.begin(e);
+    const int M = X.end(e) - row0;
+    const int rows = kDirect ? T : min(16, M - rt * 16);
+    sa[lane] = o.s0;
+    if (x1 < kS1KB * 16) sa[x1] = o.s1;
+    if (kDirect) {
+      if (threadIdx.x < 16) inv[threadIdx.x] = -1;
+      lds_barrier();
+      if (threadIdx.x < M) inv[o.ptok] = row0 + threadIdx.x;  // read after the barrier below
+    }
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < kS1KB; ++j) {
-      const v4f p = mfma_f8_16x16x128(a[j], b[j]);
-      const v4f sc = *(const v4f*)&sa[wave][j][4 * lq];
+      const v4f p = mfma_f8_16x16x128(o.a[j], b[j]);
+      const v4f sc = *(const v4f*)&sa[j * 16 + 4 * lq];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], sc[i] * sw[j], acc[i]);
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], sc[i] * o.sw[j], acc[i]);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
-    __syncthreads();
-    if (wave == 0) {
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * kWave + lane] = acc[i];
+    lds_barrier();
+    if (wave < 4) {
+      // wave i sums the partials of output rows 4q + i in wave order
+      const int i = wave;
+      float v = red[i * kWave + lane];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = red[0][i][lane];
-#pragma unroll
-        for (int w = 1; w < kS1Waves; ++w) v += red[w][i][lane];
-        // SwiGLU (moe.py:190-193): lanes r < 8 hold gate, lanes r + 8 the up column
-        const float x2 = __shfl_xor(v, 8, kWave);
-        const int r = 4 * lq + i;
-        const int prow = kDirect ? (r < rows ? inv[r] : -1) : (r < rows ? row0 + rt * 16 + r : -1);
-        if (lr < 8 && prow >= 0) {
-          const float silu = x2 / (1.0f + expf(-x2));
-          act[(size_t)prow * kI + 8 * cg + lr] = f32_to_bf16_rne(silu * v);
-        }
-      }
+      for (int w = 1; w < kS1Waves; ++w) v += red[(w * 4 + i) * kWave + lane];
+      // SwiGLU (moe.py:190-193): lanes r < 8 hold gate, lanes r + 8 the up column
+      const float x2 = __shfl_xor(v, 8, kWave);
+      const int r = 4 * lq + i;
+      const int prow = kDirect ? (r < rows ? inv[r] : -1) : (r < rows ? row0 + rt * 16 + r : -1);
+      const float silu = x2 / (1.0f + expf(-x2));
+      out.v = f32_to_bf16_rne(silu * v);
+      out.row = lr < 8 ? prow : -1;
     }
+    lds_barrier();  // red / sa / inv consumed before they are rewritten
+  };
+  auto store_out = [&](int item, const S1Out& out) {
+    if (wave < 4 && out.row >= 0) act[(size_t)out.row * kI + 8 * (item % kS1Groups) + lr] = out.v;
   };
 
-  // Row tile 0 in straight-line code: its token index load goes out first and
-  // the weight loads right after it, so waiting for the index (in-order vmcnt)
-  // leaves every weight load in flight.
-  const int tok0 = tile_token(0);
-  {
-    // this kernel's own K order: lane quarter q holds K bytes 32q .. 32q+31
-    // (measured faster than the 64-byte-run order for streaming from HBM)
-    const uint8_t* bp = w13 + ((size_t)e * k2I + n) * kH + kb0 * kBlk + 32 * lq;
-#pragma unroll
-    for (int j = 0; j < kS1KB; ++j) b[j] = *(const v8i*)(bp + j * kBlk);
-    const float* sp = w13_scale + ((size_t)e * kN2IBlk + n / kBlk) * kNHBlk + kb0;
-#pragma unroll
-    for (int j = 0; j < kS1KB; ++j) sw[j] = sp[j];
+  // Persistent: the grid is at most what fits on the device at once, and
+  // each workgroup takes a contiguous range of the (active expert, column
+  // group) items, so no workgroup is launched for an expert without rows and
+  // consecutive items of a workgroup mostly share their expert, whose row
+  // operands then stay in registers.  Each item starts by waiting for its
+  // weights and operands (issued during the previous item), moves the
+  // weights LDS -> registers, and at once sends out the next item's weight
+  // copy and loads, which stream while this item is multiplied, reduced and
+  // stored.
+  const int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int i0 = blockIdx.x * per;
+  const int i1 = min(items, i0 + per);
+  S1TileOps cur;
+  S1Out pend;       // the previous tile's outputs, stored once the next loads are out
+  if (i0 < i1) {
+    copy_w(i0);
+    issue_rows(i0, 0, cur);
+    issue_sw(i0, cur);
   }
-  row_tile(0, tok0);
-  if (!kDirect) {
 #pragma unroll 1
-    for (int rt = 1; rt * 16 < M; ++rt) {
-      const int tok = tile_token(rt);
-      __syncthreads();  // sa / red of the previous tile consumed
-      row_tile(rt, tok);
+  for (int item = i0; item < i1; ++item) {
+    wait_vmcnt_lgkm0<0>();
+    asm volatile("" ::: "memory");
+    // fragment of block j: lane (q, r) holds row r, K bytes 32q .. 32q+31
+    v8i b[kS1KB];
+    const int slot_lo = wide_slot(lr, 2 * lq), slot_hi = wide_slot(lr, 2 * lq + 1);
+#pragma unroll
+    for (int j = 0; j < kS1KB; ++j) {
+      const v4i lo = *(const v4i*)(wbuf + 2 * j * 1024 + slot_lo);
+      const v4i hi = *(const v4i*)(wbuf + 2 * j * 1024 + slot_hi);
+      b[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the buffer is read: free for the next copy
+    S1TileOps nxt = cur;
+    if (item + 1 < i1) {
+      copy_w(item + 1);
+      if ((item + 1) / kS1Groups != item / kS1Groups) issue_rows(item + 1, 0, nxt);
+      issue_sw(item + 1, nxt);
+    }
+    if (item != i0) store_out(item - 1, pend);
+    compute_tile(item, 0, cur, b, pend);
+    if (!kDirect) {
+      const int e = nth_set_bit(active, item / kS1Groups);
+#pragma unroll 1
+      for (int rt = 1; rt * 16 < X.end(e) - X.begin(e); ++rt) {
+        S1TileOps o;
+        issue_rows(item, rt, o);
+#pragma unroll
+        for (int j = 0; j < kS1KB; ++j) o.sw[j] = cur.sw[j];
+        wait_vmcnt_lgkm0<0>();  // also the next item's copy: experts of > 16 rows are rare here
+        asm volatile("" ::: "memory");
+        store_out(item, pend);
+        compute_tile(item, rt, o, b, pend);
+      }
+    }
+    cur = nxt;
   }
+  if (i0 < i1) store_out(i1 - 1, pend);
 }
 
 // ---------------------------------------------------------------------------
@@ -637,12 +730,15 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const u
   uint16_t* act = (uint16_t*)(ws + L.act);
   if (T <= kGemm1StreamMaxTokens) {
     const int max_active = min(kELocal, T * kTopK);
-    if (T <= kGemm1DirectMaxTokens)
-      hipLaunchKernelGGL(gemm1_stream_kernel<true>, dim3(max_active * kS1Groups), dim3(kS1Threads), 0, stream,
-                         hs, hs_scale, T, w13, w13_scale, off, perm, act);
-    else
-      hipLaunchKernelGGL(gemm1_stream_kernel<false>, dim3(max_active * kS1Groups), dim3(kS1Threads), 0, stream,
-                         hs, hs_scale, T, w13, w13_scale, off, perm, act);
+    if (T <= kGemm1DirectMaxTokens) {
+      static ResidentGrid grid(gemm1_stream_kernel<true>, kS1Threads);
+      hipLaunchKernelGGL(gemm1_stream_kernel<true>, dim3(grid.limit(max_active * kS1Groups)), dim3(kS1Threads), 0,
+                         stream, hs, hs_scale, T, w13, w13_scale, off, perm, act);
+    } else {
+      static ResidentGrid grid(gemm1_stream_kernel<false>, kS1Threads);
+      hipLaunchKernelGGL(gemm1_stream_kernel<false>, dim3(grid.limit(max_active * kS1Groups)), dim3(kS1Threads), 0,
+                         stream, hs, hs_scale, T, w13, w13_scale, off, perm, act);
+    }
     return hipGetLastError();
   }
   if (T < kGemm1TiledLargeMinTokens) return launch_gemm1_tiled<4, 2, 1>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);

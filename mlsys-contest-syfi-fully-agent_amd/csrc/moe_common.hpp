@@ -245,6 +245,13 @@ __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Workgroup barrier for LDS hand-offs only: this wave's LDS accesses are
+// complete, its vector-memory loads and copies may still be in flight
+// (__syncthreads would wait for those too).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // XCD-aware block -> tile map.  Workgroups are dispatched round-robin over the
 // 8 XCDs (block b runs on XCD b % 8), so block b takes tile
 //   (b % 8) * ceil(R / 8) + b / 8
@@ -255,6 +262,29 @@ __device__ __forceinline__ int xcd_tile(int b, int R) {
   const int per = (R + 7) / 8;
   const int t = (b % 8) * per + b / 8;
   return (b < per * 8 && t < R) ? t : -1;
+}
+
+// Workgroups of one kernel that fit on the device at once (compute units x
+// resident workgroups per CU), queried once, on first use.  A persistent
+// kernel launches min(work items, this) workgroups and strides over its items.
+struct ResidentGrid {
+  int n = 0;
+  template <typename Kernel>
+  ResidentGrid(Kernel kernel, int threads, size_t dyn_lds = 0) {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, dyn_lds) == hipSuccess)
+      n = cus * (per > 0 ? per : 1);
+    if (n <= 0) n = 256;
+  }
+  int limit(int items) const { return items < n ? (items > 0 ? items : 1) : n; }
+};
+
+// Index of the k-th set bit of m (k < popcount(m)).
+__device__ __forceinline__ int nth_set_bit(uint32_t m, int k) {
+  for (int i = 0; i < k; ++i) m &= m - 1;
+  return __builtin_ctz(m);
 }
 
 // Tile order inside the run: groups of `gm` row tiles sweep all `nt` column
