@@ -53,7 +53,6 @@ __device__ __forceinline__ S2Job s2_next(const ExpertRows& X, uint32_t active, S
 }
 
 struct S2Regs {
-  v4i b[kS2KB][2];     // e4m3 W2 row bytes 64g + 16q .. +15 of each scale block
   v4i a[kS2KB][2][2];  // bf16 act: elements 64g + 16q + 8h .. +7
   float sw[kS2KB];
   int tok;           // token and weight of the row this thread combines
@@ -70,17 +69,30 @@ __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
   const int crow = row0 + min((int)(threadIdx.x >> 4) & 15, rows - 1);
   R.tok = perm_token[crow];
   R.pw = perm_w[crow];
-  const uint8_t* bp = w2 + ((size_t)j.e * kH + n0 + lr) * kI + kb0 * kBlk + 16 * lq;
   const uint16_t* ap = act + (size_t)(row0 + min(lr, rows - 1)) * kI + kb0 * kBlk + 16 * lq;
 #pragma unroll
   for (int k = 0; k < kS2KB; ++k) {
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      R.b[k][g] = *(const v4i*)(bp + k * kBlk + 64 * g);
+    for (int g = 0; g < 2; ++g)
 #pragma unroll
       for (int h = 0; h < 2; ++h) R.a[k][g][h] = *(const v4i*)(ap + k * kBlk + 64 * g + 8 * h);
-    }
     R.sw[k] = w2_scale[((size_t)j.e * kNHBlk + n0 / kBlk) * kNIBlk + kb0 + k];
+  }
+}
+
+// A job's W2 bytes of this wave (16 rows n0.., K blocks kb0, kb0 + 1) -> the
+// wave's LDS stage: per K block two wide planes (rows 0-7, 8-15), 128 bytes
+// per row, chunks swizzled, so every copy reads 8 whole 128-byte row
+// segments.  4 copies per lane.
+__device__ __forceinline__ void s2_copy_w(char* stage, S2Job j, const uint8_t* __restrict__ w2, int n0, int kb0,
+                                          int lane) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    int r, c;
+    wide_copy_lane(lane, h, r, c);
+    const uint8_t* src = w2 + ((size_t)j.e * kH + n0 + r) * kI + kb0 * kBlk + 16 * c;
+#pragma unroll
+    for (int k = 0; k < kS2KB; ++k) dma16(src + k * kBlk, stage + (2 * k + h) * 1024);
   }
 }
 
@@ -89,60 +101,100 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
                      const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
                      const int32_t* __restrict__ perm_token, const float* __restrict__ perm_w, int T,
                      uint16_t* __restrict__ out) {
-  __shared__ float outacc[kGemm2StreamMaxTokens][16];
-  __shared__ float red[kS2Waves][256];
+  // One LDS object (a second __shared__ array makes the compiler wait for
+  // every LDS DMA before any LDS read): per wave a two-stage W2 ring, then
+  // the token accumulators and the K-partials.
+  constexpr int kStage = kS2KB * 2 * 1024;                 // 4 KB per wave and job
+  constexpr int kRing = 2 * kS2Waves * kStage;
+  constexpr int kAccOff = kRing;
+  constexpr int kRedOff = kAccOff + kGemm2StreamMaxTokens * 16 * 4;
+  constexpr int kLdsBytes = kRedOff + kS2Waves * 256 * 4;
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  float* outacc = (float*)(lds + kAccOff);  // [token][16]
+  float* red = (float*)(lds + kRedOff);     // [wave][256]
   const int n0 = blockIdx.x * 16;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x & (kWave - 1);
   const int lq = lane >> 4;
   const int lr = lane & 15;
   const int kb0 = wave * kS2KB;
-  for (int i = threadIdx.x; i < T * 16; i += kS2Threads) outacc[i >> 4][i & 15] = 0.f;
+  auto stage = [&](int s) { return lds + (s * kS2Waves + wave) * kStage; };
+  for (int i = threadIdx.x; i < T * 16; i += kS2Threads) outacc[i] = 0.f;
 
   ExpertRows X;
   X.load(expert_off);
   const uint32_t active = X.active();
+  // Jobs in ascending (expert, row tile) order.  The W2 slices of the next
+  // two jobs stream into the wave's two LDS stages while one is multiplied;
+  // the act rows of the next job load into registers.
   S2Job job = s2_next(X, active, {-1, 0});
-  S2Regs cur, nxt;
-  if (job.e >= 0) s2_load(cur, job, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
-  while (job.e >= 0) {
-    const S2Job nj = s2_next(X, active, job);
-    if (nj.e >= 0) s2_load(nxt, nj, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
+  S2Job j1 = job.e >= 0 ? s2_next(X, active, job) : job;
+  S2Regs r0, r1;
+  if (job.e >= 0) {
+    s2_load(r0, job, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
+    s2_copy_w(stage(0), job, w2, n0, kb0, lane);
+  }
+  if (j1.e >= 0) s2_copy_w(stage(1), j1, w2, n0, kb0, lane);
+  // One job from stage `s` with act rows `cur`; loads the next job's act rows
+  // into `nxt` and starts the copy of the job after next into stage `s`.
+  // Issue order is always: act rows of job j, copy of job j + 1.
+  auto step = [&](int s, const S2Regs& cur, S2Regs& nxt) {
+    // This job's W2 stage and act rows have landed; the next job's W2 copy
+    // (4 per lane, issued last) may stay in flight.
+    if (j1.e >= 0)
+      wait_vmcnt_lgkm0<2 * kS2KB>();
+    else
+      wait_vmcnt_lgkm0<0>();
+    asm volatile("" ::: "memory");
+    v4i b[kS2KB][2];
+#pragma unroll
+    for (int k = 0; k < kS2KB; ++k)
+#pragma unroll
+      for (int g = 0; g < 2; ++g) b[k][g] = *(const v4i*)(stage(s) + 2 * k * 1024 + wide_slot(lr, 4 * g + lq));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the stage is read: free for the job after next
+    const S2Job j2 = j1.e >= 0 ? s2_next(X, active, j1) : j1;
+    if (j1.e >= 0) s2_load(nxt, j1, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
+    if (j2.e >= 0) s2_copy_w(stage(s), j2, w2, n0, kb0, lane);
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < kS2KB; ++k) {
       v4f p = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
-        const v4i b = cur.b[k][g];
         p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][0]),
-                               e4m3x8_to_bf16((uint32_t)b[0], (uint32_t)b[1]), p);
+                               e4m3x8_to_bf16((uint32_t)b[k][g][0], (uint32_t)b[k][g][1]), p);
         p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][1]),
-                               e4m3x8_to_bf16((uint32_t)b[2], (uint32_t)b[3]), p);
+                               e4m3x8_to_bf16((uint32_t)b[k][g][2], (uint32_t)b[k][g][3]), p);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], cur.sw[k], acc[i]);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave][(4 * lq + i) * 16 + lr] = acc[i];
-    __syncthreads();
+    for (int i = 0; i < 4; ++i) red[wave * 256 + (4 * lq + i) * 16 + lr] = acc[i];
+    lds_barrier();
     if (threadIdx.x < 256) {
       const int r = threadIdx.x >> 4, c = threadIdx.x & 15;
       const int row = X.begin(job.e) + job.rt * 16 + r;
       if (row < X.end(job.e)) {
-        float o = red[0][threadIdx.x];
+        float o = red[threadIdx.x];
 #pragma unroll
-        for (int w = 1; w < kS2Waves; ++w) o += red[w][threadIdx.x];
+        for (int w = 1; w < kS2Waves; ++w) o += red[w * 256 + threadIdx.x];
         const float p = o * cur.pw;
-        outacc[cur.tok][c] = outacc[cur.tok][c] + p;
+        outacc[cur.tok * 16 + c] = outacc[cur.tok * 16 + c] + p;
       }
     }
-    __syncthreads();
-    job = nj;
-    cur = nxt;
+    lds_barrier();
+    job = j1;
+    j1 = j2;
+  };
+#pragma unroll 1
+  while (job.e >= 0) {
+    step(0, r0, r1);
+    if (job.e < 0) break;
+    step(1, r1, r0);
   }
   for (int i = threadIdx.x; i < T * 16; i += kS2Threads)
-    out[(size_t)(i >> 4) * kH + n0 + (i & 15)] = f32_to_bf16_rne(outacc[i >> 4][i & 15]);
+    out[(size_t)(i >> 4) * kH + n0 + (i & 15)] = f32_to_bf16_rne(outacc[i]);
 }
 
 // ---------------------------------------------------------------------------
