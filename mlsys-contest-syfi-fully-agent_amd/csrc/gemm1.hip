@@ -302,7 +302,7 @@ struct G1Tiled {
   static constexpr int kStageBytes = kSOff + kWaves * kWave * 4;
   static constexpr int kWscBytes = WN * 2 * kNHBlk * 4;  // weight block scales (after the stages)
   static constexpr int kStages = 3;
-  static_assert(kStages >= 2 && kStages <= 4, "pipeline depth (wait_stages_ahead)");
+  static_assert(kStages >= 2 && kStages <= 6, "pipeline depth (wait_stages_ahead)");
   static constexpr int kPlanes = 2 * (kAFrags + kBFrags);
   static_assert(kPlanes % kWaves == 0, "planes must split evenly over waves");
   static constexpr int kPlanesPerWave = kPlanes / kWaves;
@@ -328,8 +328,13 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
   ExpertRows X;
   X.load(expert_off);
   const int mt_total = X.count_tiles(C::BM);
-  const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
-  if (t < 0) return;
+  // Persistent: the grid is at most what fits on the device at once; each
+  // workgroup walks its tiles (no workgroup is launched past the last tile).
+#pragma unroll 1
+  for (int it = 0;; ++it) {
+  const int t = xcd_tile_nth(blockIdx.x, gridDim.x, mt_total * C::kNT, it);
+  if (t < 0) break;
+  if (it > 0) block_barrier();  // every wave is done with the previous tile's LDS
   int mt, nt;
   grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
   int e, row0, rows;
@@ -498,6 +503,7 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
           act[(size_t)(row0 + r) * kI + j0 + 32 * wn + 16 * nj + lr] = f32_to_bf16_rne(silu * x1);
         }
       }
+  }
 }
 
 template <int WM, int WN, int MI>
@@ -506,7 +512,10 @@ hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, c
   using C = G1Tiled<WM, WN, MI>;
   const int64_t pairs = (int64_t)T * kTopK;
   const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
-  const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
+  static ResidentGrid resident(gemm1_tiled_kernel<WM, WN, MI>, C::kThreads);
+  const int64_t upper = ((mtiles * C::kNT + 7) / 8) * 8;
+  const int64_t cap = resident.n >= 8 ? resident.n / 8 * 8 : 8;
+  const int64_t blocks = upper < cap ? upper : cap;
   hipLaunchKernelGGL((gemm1_tiled_kernel<WM, WN, MI>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
                      stream, hs, hs_scale, T, w13, w13_scale, (const int32_t*)(ws + L.expert_off),
                      (const int32_t*)(ws + L.perm_token), (uint16_t*)(ws + L.act));

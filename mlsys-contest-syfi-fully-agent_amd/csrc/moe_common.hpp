@@ -190,7 +190,11 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 // operations each are still in flight (ahead = 0, 1, 2, 3).
 template <int per_stage>
 __device__ __forceinline__ void wait_stages_ahead(int ahead) {
-  if (ahead >= 3)
+  if (ahead >= 5)
+    wait_vmcnt_lgkm0<5 * per_stage>();
+  else if (ahead == 4)
+    wait_vmcnt_lgkm0<4 * per_stage>();
+  else if (ahead == 3)
     wait_vmcnt_lgkm0<3 * per_stage>();
   else if (ahead == 2)
     wait_vmcnt_lgkm0<2 * per_stage>();
@@ -285,6 +289,18 @@ struct ResidentGrid {
 __device__ __forceinline__ int nth_set_bit(uint32_t m, int k) {
   for (int i = 0; i < k; ++i) m &= m - 1;
   return __builtin_ctz(m);
+}
+
+// Persistent form of xcd_tile: a grid of G workgroups (a multiple of 8) over
+// R tiles.  XCD x = b % 8 still owns the tile range [x * per, (x + 1) * per);
+// its G / 8 workgroups take the range's tiles round robin, so at any time an
+// XCD's workgroups work on neighbouring tiles.  The i-th tile of workgroup b,
+// or -1 past the last.
+__device__ __forceinline__ int xcd_tile_nth(int b, int G, int R, int i) {
+  const int per = (R + 7) / 8;
+  const int l = b / 8 + i * (G / 8);
+  const int t = (b % 8) * per + l;
+  return (l < per && t < R) ? t : -1;
 }
 
 // Tile order inside the run: groups of `gm` row tiles sweep all `nt` column
