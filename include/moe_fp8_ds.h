@@ -114,7 +114,8 @@ typedef struct {
   size_t perm_w;     /* float [8T]     combination weight of each permuted row    */
   size_t act;        /* bf16  [8T, 2048] SwiGLU output rows                       */
   size_t down;       /* bf16  [8T, 7168] GEMM2 output rows                        */
-  size_t block_hist; /* int32 [ceil(T/16), 32] local-expert pairs per routing workgroup */
+  size_t block_hist; /* int32 [workgroups, 32] local-expert pairs per routing workgroup
+                        (T > 16; ceil(T/4) workgroups up to T = 1024, ceil(T/16) beyond) */
   size_t total;      /* = moe_fp8_ds_workspace_size(T)                            */
 } moe_fp8_ds_layout;
 

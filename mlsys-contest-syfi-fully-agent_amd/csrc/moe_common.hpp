@@ -51,7 +51,7 @@ inline Layout make_layout(int64_t T) {
   L.perm_w = take(rows * sizeof(float));
   L.act = take(rows * kI * sizeof(uint16_t));
   L.down = take(rows * kH * sizeof(uint16_t));
-  L.block_hist = take((size_t)((T + 15) / 16) * kELocal * sizeof(int32_t));
+  L.block_hist = take((size_t)((T + 3) / 4) * kELocal * sizeof(int32_t));  // per route workgroup (4 tokens)
   L.total = off;
   return L;
 }

@@ -29,7 +29,9 @@
 namespace moe {
 namespace {
 
-constexpr int kRouteWaves = 16;
+constexpr int kRouteWaves = 16;      // tokens per route workgroup, T <= 16 (single workgroup)
+constexpr int kRouteWavesMulti = 4;  // tokens per route workgroup, 16 < T <= kRouteMultiSmallMaxTokens
+constexpr int kRouteMultiSmallMaxTokens = 1024;
 constexpr int kRouteThreads = kRouteWaves * kWave;
 
 // Maxima of the two half-waves (lanes 0-31, 32-63) of a 32-bit key,
@@ -262,16 +264,25 @@ __device__ void scatter_chunk(const int32_t* __restrict__ ids, const float* __re
 // also builds the permutation, from LDS only (no global round trip of the
 // ids); otherwise it writes its local-expert histogram to
 // block_hist[blockIdx.x][32] for perm_kernel.
-__global__ void __launch_bounds__(kRouteThreads)
+// kW tokens per workgroup, one wave each.  kSingle (T <= 16): one workgroup
+// of 16 waves also builds the permutation.  Otherwise every workgroup writes
+// its per-expert counts to block_hist for perm_kernel.  Up to
+// kRouteMultiSmallMaxTokens tokens the workgroups have 4 waves (one wave per
+// SIMD: the routing chain of a token is a long run of dependent wave-level
+// steps, which slows down when several tokens share a SIMD, and there are
+// few tokens to spread); beyond, 16 (fewer histograms for perm_kernel to sum).
+template <int kW, bool kSingle>
+__global__ void __launch_bounds__(kW * kWave)
 route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf, int T,
              int64_t offset, int32_t* __restrict__ ids, float* __restrict__ w,
              int32_t* __restrict__ pair_row, int32_t* __restrict__ expert_off,
              int32_t* __restrict__ perm_token, float* __restrict__ perm_w, int32_t* __restrict__ block_hist) {
+  static_assert(kW == kRouteWaves || (kW == kRouteWavesMulti && !kSingle), "route workgroup shapes");
   __shared__ int hist[kELocal];
   __shared__ uint32_t tokmask[kELocal];  // bit w: this workgroup's token w chose local expert
   __shared__ int first_row[kELocal];
-  __shared__ int pair_id[kRouteWaves][kTopK];
-  __shared__ float pair_w[kRouteWaves][kTopK];
+  __shared__ int pair_id[kW][kTopK];
+  __shared__ float pair_w[kW][kTopK];
   if (threadIdx.x < kELocal) {
     hist[threadIdx.x] = 0;
     tokmask[threadIdx.x] = 0u;
@@ -280,7 +291,7 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
 
   const int lane = threadIdx.x & (kWave - 1);
   const int tw = threadIdx.x / kWave;
-  const int t = blockIdx.x * kRouteWaves + tw;
+  const int t = blockIdx.x * kW + tw;
   if (t < T) {
     int sel[kTopK];
     float wsel[kTopK];
@@ -306,7 +317,7 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
     }
   }
   __syncthreads();
-  if (gridDim.x > 1) {
+  if (!kSingle) {
     if (threadIdx.x < kELocal) block_hist[(size_t)blockIdx.x * kELocal + threadIdx.x] = hist[threadIdx.x];
     return;
   }
@@ -346,15 +357,14 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
 // the counts of the tokens before its chunk; workgroup 0 writes expert_off.
 __global__ void __launch_bounds__(kRouteThreads)
 perm_kernel(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int T, int64_t offset,
-            const int32_t* __restrict__ block_hist, int32_t* __restrict__ pair_row,
+            const int32_t* __restrict__ block_hist, int tokens_per_block, int32_t* __restrict__ pair_row,
             int32_t* __restrict__ expert_off, int32_t* __restrict__ perm_token, float* __restrict__ perm_w) {
-  constexpr int kGroups = kRouteThreads / kELocal;                 // 32
-  constexpr int kRouteBlocksPerChunk = kRouteThreads / kRouteWaves;  // 64
+  constexpr int kGroups = kRouteThreads / kELocal;  // 32
   __shared__ PermShared sh;
   __shared__ int part_tot[kGroups][kELocal];
   __shared__ int part_pre[kGroups][kELocal];
-  const int nb = (T + kRouteWaves - 1) / kRouteWaves;
-  const int first = blockIdx.x * kRouteBlocksPerChunk;
+  const int nb = (T + tokens_per_block - 1) / tokens_per_block;
+  const int first = blockIdx.x * (kRouteThreads / tokens_per_block);  // route workgroups before this chunk
   const int e = threadIdx.x % kELocal;
   const int g = threadIdx.x / kELocal;
   int tot = 0, pre = 0;
@@ -386,19 +396,29 @@ perm_kernel(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, i
 
 hipError_t launch_route(const float* logits, const uint16_t* bias, float rsf, int T, int64_t offset,
                         const Layout& L, char* ws, hipStream_t stream) {
-  const int blocks = (T + kRouteWaves - 1) / kRouteWaves;
   int32_t* ids = (int32_t*)(ws + L.topk_ids);
-  hipLaunchKernelGGL(route_kernel, dim3(blocks), dim3(kRouteThreads), 0, stream, logits, bias, rsf, T,
-                     offset, ids, (float*)(ws + L.topk_w), (int32_t*)(ws + L.pair_row),
-                     (int32_t*)(ws + L.expert_off), (int32_t*)(ws + L.perm_token),
-                     (float*)(ws + L.perm_w), (int32_t*)(ws + L.block_hist));
-  if (blocks > 1) {
-    const int chunks = (T + kRouteThreads - 1) / kRouteThreads;
-    hipLaunchKernelGGL(perm_kernel, dim3(chunks), dim3(kRouteThreads), 0, stream, (const int32_t*)ids,
-                       (const float*)(ws + L.topk_w), T, offset, (const int32_t*)(ws + L.block_hist),
-                       (int32_t*)(ws + L.pair_row), (int32_t*)(ws + L.expert_off),
-                       (int32_t*)(ws + L.perm_token), (float*)(ws + L.perm_w));
+  float* w = (float*)(ws + L.topk_w);
+  int32_t* pair_row = (int32_t*)(ws + L.pair_row);
+  int32_t* off = (int32_t*)(ws + L.expert_off);
+  int32_t* perm_token = (int32_t*)(ws + L.perm_token);
+  float* perm_w = (float*)(ws + L.perm_w);
+  int32_t* hist = (int32_t*)(ws + L.block_hist);
+  if (T <= kRouteWaves) {
+    hipLaunchKernelGGL((route_kernel<kRouteWaves, true>), dim3(1), dim3(kRouteThreads), 0, stream, logits, bias,
+                       rsf, T, offset, ids, w, pair_row, off, perm_token, perm_w, hist);
+    return hipGetLastError();
   }
+  const int tpb = T <= kRouteMultiSmallMaxTokens ? kRouteWavesMulti : kRouteWaves;
+  const int blocks = (T + tpb - 1) / tpb;
+  if (tpb == kRouteWavesMulti)
+    hipLaunchKernelGGL((route_kernel<kRouteWavesMulti, false>), dim3(blocks), dim3(kRouteWavesMulti * kWave), 0,
+                       stream, logits, bias, rsf, T, offset, ids, w, pair_row, off, perm_token, perm_w, hist);
+  else
+    hipLaunchKernelGGL((route_kernel<kRouteWaves, false>), dim3(blocks), dim3(kRouteThreads), 0, stream, logits,
+                       bias, rsf, T, offset, ids, w, pair_row, off, perm_token, perm_w, hist);
+  const int chunks = (T + kRouteThreads - 1) / kRouteThreads;
+  hipLaunchKernelGGL(perm_kernel, dim3(chunks), dim3(kRouteThreads), 0, stream, (const int32_t*)ids,
+                     (const float*)w, T, offset, (const int32_t*)hist, tpb, pair_row, off, perm_token, perm_w);
   return hipGetLastError();
 }
 

@@ -152,7 +152,9 @@ class RouteResult:
         self.perm_w = view(lay.perm_w, T * TOP_K, torch.float32)
         self.act = view(lay.act, T * TOP_K * I, torch.int16).view(T * TOP_K, I)
         self.down = view(lay.down, T * TOP_K * H, torch.int16).view(T * TOP_K, H)
-        self.block_hist = view(lay.block_hist, (T + 15) // 16 * E_LOCAL, torch.int32).view(-1, E_LOCAL)
+        # one row per routing workgroup: 4 tokens each up to T = 1024, 16 beyond
+        blocks = (T + 3) // 4 if T <= 1024 else (T + 15) // 16
+        self.block_hist = view(lay.block_hist, blocks * E_LOCAL, torch.int32).view(-1, E_LOCAL)
 
 
 def route(routing_logits, routing_bias, local_expert_offset, routed_scaling_factor, ws=None):
