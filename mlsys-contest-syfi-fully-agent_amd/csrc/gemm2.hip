@@ -504,21 +504,35 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
     v4i braw[C::NJ];
 #pragma unroll
     for (int nj = 0; nj < C::NJ; ++nj) braw[nj] = *(const v4i*)(sbuf + C::kBOff + (wn * C::NJ + nj) * 1024 + slot_b);
+    // Software-pipelined over column blocks: the scale FMAs of block nj - 1
+    // are issued after the MFMAs of block nj, so the VALU work runs while the
+    // matrix core is busy; each block's MFMA results live for one block.
+    v4f pp[C::MI];
 #pragma unroll
     for (int nj = 0; nj < C::NJ; ++nj) {
       const v4i raw = braw[nj];
       const v8bf b0 = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
       const v8bf b1 = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
+      v4f pc[C::MI];
 #pragma unroll
       for (int mi = 0; mi < C::MI; ++mi) {
-        v4f p = mfma_bf16_16x16x32(a[mi][0], b0, v4f{0.f, 0.f, 0.f, 0.f});
-        p = mfma_bf16_16x16x32(a[mi][1], b1, p);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], sb, acc[mi][nj][i]);
+        pc[mi] = mfma_bf16_16x16x32(a[mi][0], b0, v4f{0.f, 0.f, 0.f, 0.f});
+        pc[mi] = mfma_bf16_16x16x32(a[mi][1], b1, pc[mi]);
       }
-      // keep each column block's MFMA results short-lived
+      if (nj > 0) {
+#pragma unroll
+        for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[mi][nj - 1][i] = __builtin_fmaf(pp[mi][i], sb, acc[mi][nj - 1][i]);
+      }
+#pragma unroll
+      for (int mi = 0; mi < C::MI; ++mi) pp[mi] = pc[mi];
       __builtin_amdgcn_sched_barrier(0);
     }
+#pragma unroll
+    for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[mi][C::NJ - 1][i] = __builtin_fmaf(pp[mi][i], sb, acc[mi][C::NJ - 1][i]);
   };
 
   // Waves whose 64 rows all lie past the tile's rows only help with copies.
