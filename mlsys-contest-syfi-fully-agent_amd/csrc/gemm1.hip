@@ -651,36 +651,59 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
       const v4i lo = *(const v4i*)(f + slot_lo), hi = *(const v4i*)(f + slot_hi);
       return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     };
-    v8i b[2 * C::NJ];
-#pragma unroll
-    for (int nj = 0; nj < C::NJ; ++nj) {
-      b[nj] = frag(C::kBOff + (C::NJ * wn + nj) * C::kFrag);                  // gate
-      b[C::NJ + nj] = frag(C::kBOff + (8 + C::NJ * wn + nj) * C::kFrag);      // up
-    }
+    // column block nj: gate blocks 0 .. NJ-1, then the matching up blocks
+    auto bfrag = [&](int nj) {
+      return frag(C::kBOff + (nj < C::NJ ? C::NJ * wn + nj : 8 + C::NJ * wn + nj - C::NJ) * C::kFrag);
+    };
     const float sg = wsc[kb], su = wsc[kNHBlk + kb];
+    v8i a[C::MI];
+    v4f sgm[C::MI], sum[C::MI];  // row scale x gate / up weight scale
 #pragma unroll
     for (int mi = 0; mi < C::MI; ++mi) {
-      const v8i a = frag((C::MI * wm + mi) * C::kFrag);
+      a[mi] = frag((C::MI * wm + mi) * C::kFrag);
       const int r = C::MI * 16 * wm + 16 * mi + 4 * lq;  // 4 rows in one wave's scale slot
       const int slot = (r / C::kScaleRowsPerWave) * kWave + r % C::kScaleRowsPerWave;
       const v4f sa = *(const v4f*)(sb + C::kSOff + slot * 4);
-      v4f sgm, sum;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sgm[i] = sa[i] * sg;
-        sum[i] = sa[i] * su;
+        sgm[mi][i] = sa[i] * sg;
+        sum[mi][i] = sa[i] * su;
       }
-#pragma unroll
-      for (int nj = 0; nj < 2 * C::NJ; ++nj) {
-        const v4f p = mfma_f8_16x16x128(a, b[nj]);
-        const v4f sc = nj < C::NJ ? sgm : sum;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(p[i], sc[i], acc[mi][nj][i]);
-      }
-      // keep each row block's MFMA results short-lived (otherwise the
-      // scheduler hoists all 32 MFMAs and runs out of registers)
-      __builtin_amdgcn_sched_barrier(0);
     }
+    // Software-pipelined over column blocks: block nj's four MFMAs are issued
+    // first, then the scale FMAs of block nj - 1 (whose MFMAs have finished),
+    // so the VALU work runs while the matrix core is busy; block nj + 1's B
+    // fragment is read from LDS during block nj.
+    v8i bn = bfrag(0);
+    v4f pp[C::MI];
+#pragma unroll
+    for (int nj = 0; nj < 2 * C::NJ; ++nj) {
+      // two halves (row blocks 0-1, 2-3), so that only half of the previous
+      // block's results are still live when this block's last MFMAs issue
+      v4f pc[C::MI];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int mi = 2 * h; mi < 2 * h + 2; ++mi) pc[mi] = mfma_f8_16x16x128(a[mi], bn);
+        if (h == 1 && nj + 1 < 2 * C::NJ) bn = bfrag(nj + 1);
+        if (nj > 0) {
+#pragma unroll
+          for (int mi = 2 * h; mi < 2 * h + 2; ++mi) {
+            const v4f sc = nj - 1 < C::NJ ? sgm[mi] : sum[mi];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mi][nj - 1][i] = __builtin_fmaf(pp[mi][i], sc[i], acc[mi][nj - 1][i]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int mi = 0; mi < C::MI; ++mi) pp[mi] = pc[mi];
+    }
+#pragma unroll
+    for (int mi = 0; mi < C::MI; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[mi][2 * C::NJ - 1][i] = __builtin_fmaf(pp[mi][i], sum[mi][i], acc[mi][2 * C::NJ - 1][i]);
   };
 
   // Waves whose 64 rows all lie past the tile's rows (small experts) only
