@@ -513,11 +513,13 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
       const v4i raw = braw[nj];
       const v8bf b0 = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
       const v8bf b1 = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
+      // operands swapped (W2 rows as the MFMA's A): lane (q, r) receives
+      // row r, columns 4q .. 4q+3 of the block, stored as one 8-byte write
       v4f pc[C::MI];
 #pragma unroll
       for (int mi = 0; mi < C::MI; ++mi) {
-        pc[mi] = mfma_bf16_16x16x32(a[mi][0], b0, v4f{0.f, 0.f, 0.f, 0.f});
-        pc[mi] = mfma_bf16_16x16x32(a[mi][1], b1, pc[mi]);
+        pc[mi] = mfma_bf16_16x16x32(b0, a[mi][0], v4f{0.f, 0.f, 0.f, 0.f});
+        pc[mi] = mfma_bf16_16x16x32(b1, a[mi][1], pc[mi]);
       }
       if (nj > 0) {
 #pragma unroll
@@ -559,15 +561,19 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
   if (wave_live) compute(C::kSteps - 1);
 
 #pragma unroll
-  for (int mi = 0; mi < C::MI; ++mi)
+  for (int mi = 0; mi < C::MI; ++mi) {
+    const int r = (wm * C::MI + mi) * 16 + lr;
+    if (r < rows) {
+      uint16_t* drow = down + (size_t)(row0 + r) * kH + n0 + 16 * wn * C::NJ + 4 * lq;
 #pragma unroll
-    for (int nj = 0; nj < C::NJ; ++nj)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = (wm * C::MI + mi) * 16 + 4 * lq + i;
-        if (r < rows)
-          down[(size_t)(row0 + r) * kH + n0 + 16 * (wn * C::NJ + nj) + lr] = f32_to_bf16_rne(acc[mi][nj][i]);
+      for (int nj = 0; nj < C::NJ; ++nj) {
+        uint2 v;
+        v.x = (uint32_t)f32_to_bf16_rne(acc[mi][nj][0]) | ((uint32_t)f32_to_bf16_rne(acc[mi][nj][1]) << 16);
+        v.y = (uint32_t)f32_to_bf16_rne(acc[mi][nj][2]) | ((uint32_t)f32_to_bf16_rne(acc[mi][nj][3]) << 16);
+        *(uint2*)(drow + 16 * nj) = v;
       }
+    }
+  }
 }
 
 hipError_t launch_gemm2_wide(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
