@@ -656,19 +656,19 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
       return frag(C::kBOff + (nj < C::NJ ? C::NJ * wn + nj : 8 + C::NJ * wn + nj - C::NJ) * C::kFrag);
     };
     const float sg = wsc[kb], su = wsc[kNHBlk + kb];
+    // Operands swapped (W13 rows as the MFMA's A): lane (q, r) receives row
+    // r, columns 4q .. 4q+3 of each block, so one row scale per lane and row
+    // block, and the epilogue stores 4 adjacent columns at once.
     v8i a[C::MI];
-    v4f sgm[C::MI], sum[C::MI];  // row scale x gate / up weight scale
+    float sgm[C::MI], sum[C::MI];  // row scale x gate / up weight scale
 #pragma unroll
     for (int mi = 0; mi < C::MI; ++mi) {
       a[mi] = frag((C::MI * wm + mi) * C::kFrag);
-      const int r = C::MI * 16 * wm + 16 * mi + 4 * lq;  // 4 rows in one wave's scale slot
+      const int r = C::MI * 16 * wm + 16 * mi + lr;
       const int slot = (r / C::kScaleRowsPerWave) * kWave + r % C::kScaleRowsPerWave;
-      const v4f sa = *(const v4f*)(sb + C::kSOff + slot * 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sgm[mi][i] = sa[i] * sg;
-        sum[mi][i] = sa[i] * su;
-      }
+      const float sa = *(const float*)(sb + C::kSOff + slot * 4);
+      sgm[mi] = sa * sg;
+      sum[mi] = sa * su;
     }
     // Software-pipelined over column blocks: block nj's four MFMAs are issued
     // first, then the scale FMAs of block nj - 1 (whose MFMAs have finished),
@@ -684,14 +684,14 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int mi = 2 * h; mi < 2 * h + 2; ++mi) pc[mi] = mfma_f8_16x16x128(a[mi], bn);
+        for (int mi = 2 * h; mi < 2 * h + 2; ++mi) pc[mi] = mfma_f8_16x16x128(bn, a[mi]);
         if (h == 1 && nj + 1 < 2 * C::NJ) bn = bfrag(nj + 1);
         if (nj > 0) {
 #pragma unroll
           for (int mi = 2 * h; mi < 2 * h + 2; ++mi) {
-            const v4f sc = nj - 1 < C::NJ ? sgm[mi] : sum[mi];
+            const float sc = nj - 1 < C::NJ ? sgm[mi] : sum[mi];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mi][nj - 1][i] = __builtin_fmaf(pp[mi][i], sc[i], acc[mi][nj - 1][i]);
+            for (int i = 0; i < 4; ++i) acc[mi][nj - 1][i] = __builtin_fmaf(pp[mi][i], sc, acc[mi][nj - 1][i]);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -703,7 +703,7 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
     for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        acc[mi][2 * C::NJ - 1][i] = __builtin_fmaf(pp[mi][i], sum[mi][i], acc[mi][2 * C::NJ - 1][i]);
+        acc[mi][2 * C::NJ - 1][i] = __builtin_fmaf(pp[mi][i], sum[mi], acc[mi][2 * C::NJ - 1][i]);
   };
 
   // Waves whose 64 rows all lie past the tile's rows (small experts) only
@@ -727,18 +727,23 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
 
   // ---- SwiGLU epilogue (moe.py:190-193): act = silu(up) * gate ------------
 #pragma unroll
-  for (int mi = 0; mi < C::MI; ++mi)
+  for (int mi = 0; mi < C::MI; ++mi) {
+    const int r = C::MI * 16 * wm + 16 * mi + lr;
+    if (r < rows) {
+      uint16_t* arow = act + (size_t)(row0 + r) * kI + j0 + 16 * C::NJ * wn + 4 * lq;
 #pragma unroll
-    for (int nj = 0; nj < C::NJ; ++nj)
+      for (int nj = 0; nj < C::NJ; ++nj) {
+        uint32_t h[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = C::MI * 16 * wm + 16 * mi + 4 * lq + i;
-        if (r < rows) {
+        for (int i = 0; i < 4; ++i) {
           const float x1 = acc[mi][nj][i], x2 = acc[mi][C::NJ + nj][i];
           const float silu = x2 / (1.0f + expf(-x2));
-          act[(size_t)(row0 + r) * kI + j0 + 16 * (C::NJ * wn + nj) + lr] = f32_to_bf16_rne(silu * x1);
+          h[i] = f32_to_bf16_rne(silu * x1);
         }
+        *(uint2*)(arow + 16 * nj) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
       }
+    }
+  }
 }
 
 hipError_t launch_gemm1_wide(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
