@@ -12,8 +12,8 @@
 //     one half-wave in one register slot;
 //   * scores become 32-bit order-preserving keys; the group top-2 sums use
 //     DPP max-reductions per half-wave (four slots in parallel), and the
-//     top-8 is a radix select on the keys (one ballot count per bit) followed
-//     by ballots that take the tied keys in ascending expert order;
+//     top-8 is eight rounds of a DPP wave maximum plus ballots for the lowest
+//     expert holding it, the ids then sorted by a comparator network;
 //   * T <= 16 (decode): the single workgroup also builds the permutation from
 //     LDS (per-expert token bitmasks), with no global atomics, fences or
 //     re-reads of the ids;
@@ -36,14 +36,25 @@ constexpr int kRouteThreads = kRouteWaves * kWave;
 
 // Maxima of the two half-waves (lanes 0-31, 32-63) of a 32-bit key,
 // wave-uniform.  Four DPP row steps, then rows 1 and 3 take rows 0 and 2.
+// Maximum over the wave, wave-uniform: DPP maxima within each row of 16
+// (bound_ctrl moves, which the compiler folds into v_max_u32_dpp), then the
+// four row maxima.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
+  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppQuad1032, 0xF, 0xF, true));
+  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppQuad2301, 0xF, 0xF, true));
+  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppRowHalfMirror, 0xF, 0xF, true));
+  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppRowMirror, 0xF, 0xF, true));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)k, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)k, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
+  return max(max(a, b), max(c, d));
+}
+
 __device__ __forceinline__ void halfwave_max(uint32_t k, uint32_t& m0, uint32_t& m1) {
   k = row16_max_u32(k);
   k = max(k, dpp_u32<kDppRowBcast15, 0xA>(k));
   m0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 31);
   m1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
 }
-
-__device__ __forceinline__ int popc_ballot(bool p) { return __popcll(__ballot(p)); }
 
 // Routes token t with one wavefront.  Returns the 8 selected ids, ascending
 // (wave-uniform), and their weights (wave-uniform).
@@ -94,48 +105,56 @@ __device__ void route_token(const float* __restrict__ logits, const uint16_t* __
     for (int h = 0; h < kNGroup; ++h) rank += (G[h] > G[g]) || (G[h] == G[g] && h < g);
     keep |= (rank < kTopKGroup ? 1u : 0u) << g;
   }
-  // moe.py:149-151: top-8 experts among the kept groups.  theta = the 8th
-  // largest key (radix select: the largest value v with count(key >= v) >= 8,
-  // one bit at a time from the top); take every key > theta and, of the keys
-  // equal to theta, the lowest expert indices.
+  // moe.py:149-151: top-8 experts among the kept groups, as eight rounds of
+  // (wave maximum of the keys, the lowest expert index holding it); the
+  // expert taken leaves the round's candidates.  This is the set "every key
+  // above the 8th largest, then the lowest indices among the keys equal to
+  // it" (keys of dropped groups are 0, below every real score).
   const int half = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     if (!((keep >> (2 * j + half)) & 1u)) key[j] = 0u;
-  uint32_t theta = 0;
-#pragma unroll
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t cand = theta | (1u << b);
-    const int cnt = popc_ballot(key[0] >= cand) + popc_ballot(key[1] >= cand) + popc_ballot(key[2] >= cand) +
-                    popc_ballot(key[3] >= cand);
-    if (cnt >= kTopK) theta = cand;
-  }
-  uint64_t pick[4];
-  int need = kTopK;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    pick[j] = __ballot(key[j] > theta);
-    need -= __popcll(pick[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint64_t eq = __ballot(key[j] == theta);
-    while (need > 0 && eq) {
-      pick[j] |= eq & (~eq + 1);  // lowest remaining lane
-      eq &= eq - 1;
-      --need;
-    }
-  }
-  // ids ascending = slot-major, lane-minor order of the picked bits (all
-  // wave-uniform; the loop is unrolled so every index is static)
+  uint32_t taken = 0u;  // bit j: this lane's expert 64j + lane already taken
+  int pick[kTopK];
 #pragma unroll
   for (int r = 0; r < kTopK; ++r) {
-    const int j = pick[0] ? 0 : pick[1] ? 1 : pick[2] ? 2 : 3;
-    const uint64_t m = j == 0 ? pick[0] : j == 1 ? pick[1] : j == 2 ? pick[2] : pick[3];
-    const int l = m ? __builtin_ctzll(m) : 0;  // m != 0 whenever 8 keys are nonzero
-    const uint64_t rest = m & (m - 1);
-    if (j == 0) pick[0] = rest; else if (j == 1) pick[1] = rest; else if (j == 2) pick[2] = rest; else pick[3] = rest;
-    sel[r] = 64 * j + l;
+    const uint32_t M = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+    // slot j: lanes holding M (taken experts hold 0, so only a zero maximum
+    // needs the taken bits)
+    uint64_t b[4];
+    if (M != 0u) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = __ballot(key[j] == M);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = __ballot(key[j] == 0u && !((taken >> j) & 1u));
+    }
+    // lowest expert index 64j + lane among them
+    int t = 4 * kWave;
+#pragma unroll
+    for (int j = 3; j >= 0; --j)
+      if (b[j]) t = 64 * j + __builtin_ctzll(b[j]);
+    pick[r] = t;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (64 * j + lane == t) {
+        key[j] = 0u;
+        taken |= 1u << j;
+      }
+  }
+  // ids ascending: Batcher's 19-comparator network on the (wave-uniform) ids
+  constexpr int kNet[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
+                               {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+  for (int c = 0; c < 19; ++c) {
+    const int x = pick[kNet[c][0]], y = pick[kNet[c][1]];
+    pick[kNet[c][0]] = min(x, y);
+    pick[kNet[c][1]] = max(x, y);
+  }
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    const int j = pick[r] >> 6, l = pick[r] & 63;
+    sel[r] = pick[r];
     const float sj = j == 0 ? s[0] : j == 1 ? s[1] : j == 2 ? s[2] : s[3];
     wsel[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), l));
   }
