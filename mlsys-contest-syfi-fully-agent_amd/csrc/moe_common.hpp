@@ -229,8 +229,14 @@ constexpr int kDppRowBcast15 = 0x142;
 
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  // lanes outside ROW_MASK keep their own value (old = v)
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROW_MASK, 0xF, false);
+  if constexpr (ROW_MASK == 0xF) {
+    // every lane reads a lane of its own row (quad permutes, row mirrors):
+    // a bound_ctrl move, which the compiler folds into the consuming VALU op
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+  } else {
+    // lanes outside ROW_MASK keep their own value (old = v)
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROW_MASK, 0xF, false);
+  }
 }
 
 // Maximum of a 32-bit value over each row of 16 lanes, in every lane of the row.
