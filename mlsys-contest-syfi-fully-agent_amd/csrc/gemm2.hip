@@ -493,6 +493,11 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
 
   auto compute = [&](int s) {
     const char* sbuf = lds + (s % C::kStages) * C::kStageBytes;
+    auto bread = [&](int nj) { return *(const v4i*)(sbuf + C::kBOff + (wn * C::NJ + nj) * 1024 + slot_b); };
+    // LDS reads in the order of first use, B fragments two blocks ahead: the
+    // first MFMAs wait only for their own operands
+    v4i braw[C::NJ];
+    braw[0] = bread(0);
     v8bf a[C::MI][2];
 #pragma unroll
     for (int mi = 0; mi < C::MI; ++mi) {
@@ -500,16 +505,15 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
       a[mi][0] = *(const v8bf*)(f + slot_a0);
       a[mi][1] = *(const v8bf*)(f + slot_a1);
     }
+    braw[1] = bread(1);
     const float sb = wsc[wn * kNIBlk + (s >> 1)];
-    v4i braw[C::NJ];
-#pragma unroll
-    for (int nj = 0; nj < C::NJ; ++nj) braw[nj] = *(const v4i*)(sbuf + C::kBOff + (wn * C::NJ + nj) * 1024 + slot_b);
     // Software-pipelined over column blocks: the scale FMAs of block nj - 1
     // are issued after the MFMAs of block nj, so the VALU work runs while the
     // matrix core is busy; each block's MFMA results live for one block.
     v4f pp[C::MI];
 #pragma unroll
     for (int nj = 0; nj < C::NJ; ++nj) {
+      if (nj + 2 < C::NJ) braw[nj + 2] = bread(nj + 2);
       const v4i raw = braw[nj];
       const v8bf b0 = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
       const v8bf b1 = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
