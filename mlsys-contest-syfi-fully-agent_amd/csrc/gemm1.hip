@@ -368,7 +368,9 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
       dst[k] = C::kBOff + bf * C::kFrag + half * 1024;
     }
   }
-  const int srow = wave * C::kScaleRowsPerWave + lane;
+  // lanes past the wave's rows copy the first row's scale again (one cache
+  // line instead of one per lane; their slot entries are never read)
+  const int srow = wave * C::kScaleRowsPerWave + (lane < C::kScaleRowsPerWave ? lane : 0);
   const float* ssrc = hs_scale + perm_token[row0 + min(srow, rows - 1)];
   const int sdst = C::kSOff + wave * kWave * 4;
 
@@ -615,7 +617,10 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
       dst[k] = C::kBOff + bf * C::kFrag + half * 1024;
     }
   }
-  const uint32_t stok = (uint32_t)perm_token[row0 + min(wave * C::kScaleRowsPerWave + lane, rows - 1)];
+  // lanes past the wave's rows copy the first row's scale again (their slot
+  // entries are never read)
+  const uint32_t stok =
+      (uint32_t)perm_token[row0 + min(wave * C::kScaleRowsPerWave + (lane < C::kScaleRowsPerWave ? lane : 0), rows - 1)];
   const int sdst = C::kSOff + wave * kWave * 4;
 
   auto issue = [&](int kb) {
