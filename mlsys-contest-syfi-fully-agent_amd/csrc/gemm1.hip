@@ -660,26 +660,31 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
     auto bfrag = [&](int nj) {
       return frag(C::kBOff + (nj < C::NJ ? C::NJ * wn + nj : 8 + C::NJ * wn + nj - C::NJ) * C::kFrag);
     };
-    const float sg = wsc[kb], su = wsc[kNHBlk + kb];
     // Operands swapped (W13 rows as the MFMA's A): lane (q, r) receives row
     // r, columns 4q .. 4q+3 of each block, so one row scale per lane and row
-    // block, and the epilogue stores 4 adjacent columns at once.
+    // block, and the epilogue stores 4 adjacent columns at once.  LDS reads
+    // in order of first use: block 0's B fragment and the A fragments, then,
+    // behind block 0's MFMAs, the scales (first needed one block later).
+    v8i bn = bfrag(0);
     v8i a[C::MI];
-    float sgm[C::MI], sum[C::MI];  // row scale x gate / up weight scale
 #pragma unroll
-    for (int mi = 0; mi < C::MI; ++mi) {
-      a[mi] = frag((C::MI * wm + mi) * C::kFrag);
-      const int r = C::MI * 16 * wm + 16 * mi + lr;
-      const int slot = (r / C::kScaleRowsPerWave) * kWave + r % C::kScaleRowsPerWave;
-      const float sa = *(const float*)(sb + C::kSOff + slot * 4);
-      sgm[mi] = sa * sg;
-      sum[mi] = sa * su;
-    }
+    for (int mi = 0; mi < C::MI; ++mi) a[mi] = frag((C::MI * wm + mi) * C::kFrag);
+    float sgm[C::MI], sum[C::MI];  // row scale x gate / up weight scale
+    auto read_scales = [&]() {
+      const float sg = wsc[kb], su = wsc[kNHBlk + kb];
+#pragma unroll
+      for (int mi = 0; mi < C::MI; ++mi) {
+        const int r = C::MI * 16 * wm + 16 * mi + lr;
+        const int slot = (r / C::kScaleRowsPerWave) * kWave + r % C::kScaleRowsPerWave;
+        const float sa = *(const float*)(sb + C::kSOff + slot * 4);
+        sgm[mi] = sa * sg;
+        sum[mi] = sa * su;
+      }
+    };
     // Software-pipelined over column blocks: block nj's four MFMAs are issued
     // first, then the scale FMAs of block nj - 1 (whose MFMAs have finished),
     // so the VALU work runs while the matrix core is busy; block nj + 1's B
     // fragment is read from LDS during block nj.
-    v8i bn = bfrag(0);
     v4f pp[C::MI];
 #pragma unroll
     for (int nj = 0; nj < 2 * C::NJ; ++nj) {
@@ -691,6 +696,7 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
 #pragma unroll
         for (int mi = 2 * h; mi < 2 * h + 2; ++mi) pc[mi] = mfma_f8_16x16x128(bn, a[mi]);
         if (h == 1 && nj + 1 < 2 * C::NJ) bn = bfrag(nj + 1);
+        if (h == 1 && nj == 0) read_scales();
         if (nj > 0) {
 #pragma unroll
           for (int mi = 2 * h; mi < 2 * h + 2; ++mi) {
