@@ -16,7 +16,7 @@
 //   * streaming (small T): one workgroup per (expert, 8-column group), weights
 //     read once straight into registers -- HBM-bound;
 //   * tiled (large T): LDS-staged operand tiles, DMA pipeline -- MFMA-bound.
-#include "moe_common.hpp"
+#include "route_token.hpp"
 
 namespace moe {
 namespace {
@@ -64,12 +64,24 @@ struct S1Out {
   int row;  // destination act row, -1: none
 };
 
+// kDirect: the workgroup routes the T tokens itself (route_small, from the
+// routing inputs in `dr`) instead of reading a routing launch's results;
+// workgroup 0 also writes them to the workspace for GEMM2 and the caller.
+struct DirectRoute {
+  const float* logits;
+  const uint16_t* bias;
+  float rsf;
+  int64_t offset;
+  RouteOut out;
+};
+static_assert(kGemm1DirectMaxTokens == kSmallRouteMaxTokens, "the decode path routes in GEMM1");
+
 template <bool kDirect>
 __global__ void __launch_bounds__(kS1Threads)
 gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
                     const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                     const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
-                    uint16_t* __restrict__ act) {
+                    uint16_t* __restrict__ act, DirectRoute dr) {
   // Per wave: the weights of the item being started (copy j of lane l at
   // 1024 j + 16 l; the only LDS DMA target), the activation scales and the
   // K-partials.  The permutation (<= 8 * 64 rows) is cached whole.
@@ -80,13 +92,22 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
   constexpr int kRedOff = kSaOff + kS1Waves * kS1KB * 16 * 4;
   constexpr int kInvOff = kRedOff + kS1Waves * 4 * kWave * 4;
   constexpr int kPermOff = kInvOff + 16 * 4;
-  constexpr int kLdsBytes = kPermOff + kTopK * kGemm1StreamMaxTokens * 4;
+  constexpr int kSrOff = kPermOff + kTopK * kGemm1StreamMaxTokens * 4;  // kDirect: the routing
+  constexpr int kLdsBytes = kSrOff + (kDirect ? (int)sizeof(SmallRoute) : 0);
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
   float* red = (float*)(lds + kRedOff);
   int* inv = (int*)(lds + kInvOff);                  // kDirect: token -> permuted row, -1 if none
   int* perm_lds = (int*)(lds + kPermOff);
+  const int32_t* eoff = expert_off;
+  const int32_t* ptok_src = perm_token;
+  if constexpr (kDirect) {
+    SmallRoute& sr = *(SmallRoute*)(lds + kSrOff);
+    route_small(dr.logits, dr.bias, dr.rsf, T, dr.offset, sr, dr.out, blockIdx.x == 0);
+    eoff = sr.expert_off;
+    ptok_src = sr.perm_token;
+  }
   ExpertRows X;
-  X.load(expert_off);
+  X.load(eoff);
   const uint32_t active = X.active();
   const int items = __popc(active) * kS1Groups;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -145,7 +166,7 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
 #pragma unroll
     for (int j = 0; j < kS1KB; ++j) o.a[j] = *(const v8i*)(ap + j * kBlk);
     o.ptok = 0;
-    if (kDirect && (int)threadIdx.x < X.end(e) - X.begin(e)) o.ptok = perm_token[X.begin(e) + threadIdx.x];
+    if (kDirect && (int)threadIdx.x < X.end(e) - X.begin(e)) o.ptok = ptok_src[X.begin(e) + threadIdx.x];
   };
   // The item's weight block scales (this lane's column).
   auto issue_sw = [&](int item, S1TileOps& o) {
@@ -771,21 +792,28 @@ hipError_t launch_gemm1_wide(const uint8_t* hs, const float* hs_scale, int T, co
 
 }  // namespace
 
+bool gemm1_routes(int T) { return T <= kGemm1DirectMaxTokens; }
+
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
-                        const float* w13_scale, const Layout& L, char* ws, hipStream_t stream) {
+                        const float* w13_scale, const float* logits, const uint16_t* bias, float rsf,
+                        int64_t offset, const Layout& L, char* ws, hipStream_t stream) {
   const int32_t* off = (const int32_t*)(ws + L.expert_off);
   const int32_t* perm = (const int32_t*)(ws + L.perm_token);
   uint16_t* act = (uint16_t*)(ws + L.act);
   if (T <= kGemm1StreamMaxTokens) {
     const int max_active = min(kELocal, T * kTopK);
-    if (T <= kGemm1DirectMaxTokens) {
+    if (gemm1_routes(T)) {
+      const DirectRoute dr{logits, bias, rsf, offset,
+                           RouteOut{(int32_t*)(ws + L.topk_ids), (float*)(ws + L.topk_w), (int32_t*)(ws + L.pair_row),
+                                    (int32_t*)(ws + L.expert_off), (int32_t*)(ws + L.perm_token),
+                                    (float*)(ws + L.perm_w)}};
       static ResidentGrid grid(gemm1_stream_kernel<true>, kS1Threads);
       hipLaunchKernelGGL(gemm1_stream_kernel<true>, dim3(grid.limit(max_active * kS1Groups)), dim3(kS1Threads), 0,
-                         stream, hs, hs_scale, T, w13, w13_scale, off, perm, act);
+                         stream, hs, hs_scale, T, w13, w13_scale, off, perm, act, dr);
     } else {
       static ResidentGrid grid(gemm1_stream_kernel<false>, kS1Threads);
       hipLaunchKernelGGL(gemm1_stream_kernel<false>, dim3(grid.limit(max_active * kS1Groups)), dim3(kS1Threads), 0,
-                         stream, hs, hs_scale, T, w13, w13_scale, off, perm, act);
+                         stream, hs, hs_scale, T, w13, w13_scale, off, perm, act, DirectRoute{});
     }
     return hipGetLastError();
   }

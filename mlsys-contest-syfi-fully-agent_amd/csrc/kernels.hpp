@@ -7,8 +7,13 @@ namespace moe {
 
 hipError_t launch_route(const float* logits, const uint16_t* bias, float rsf, int T, int64_t offset,
                         const Layout& L, char* ws, hipStream_t stream);
+// T <= 16: GEMM1 routes the tokens itself (each workgroup, from LDS; workgroup
+// 0 writes the routing results to the workspace), so no launch_route runs
+// before it.  The routing inputs are unused for larger T.
+bool gemm1_routes(int T);
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
-                        const float* w13_scale, const Layout& L, char* ws, hipStream_t stream);
+                        const float* w13_scale, const float* logits, const uint16_t* bias, float rsf,
+                        int64_t offset, const Layout& L, char* ws, hipStream_t stream);
 // Largest T for which GEMM2 also performs the weighted combine (no combine pass).
 constexpr int kGemm2StreamMaxTokens = 64;
 bool gemm2_fuses_combine(int T);

@@ -105,14 +105,14 @@ static int run_layer(const float* routing_logits, const void* routing_bias, cons
     if (events && err == hipSuccess) err = hipEventRecord(events[i], stream);
   };
   mark(0);
-  err = err != hipSuccess ? err
-                          : moe::launch_route(routing_logits, (const uint16_t*)routing_bias,
-                                              (float)routed_scaling_factor, t, local_expert_offset,
-                                              L, ws, stream);
+  if (err == hipSuccess && !moe::gemm1_routes(t))
+    err = moe::launch_route(routing_logits, (const uint16_t*)routing_bias, (float)routed_scaling_factor, t,
+                            local_expert_offset, L, ws, stream);
   mark(1);
   if (err == hipSuccess)
-    err = moe::launch_gemm1((const uint8_t*)hidden_states, hidden_states_scale, t,
-                            (const uint8_t*)gemm1_weights, gemm1_weights_scale, L, ws, stream);
+    err = moe::launch_gemm1((const uint8_t*)hidden_states, hidden_states_scale, t, (const uint8_t*)gemm1_weights,
+                            gemm1_weights_scale, routing_logits, (const uint16_t*)routing_bias,
+                            (float)routed_scaling_factor, local_expert_offset, L, ws, stream);
   mark(2);
   if (err == hipSuccess)
     err = moe::launch_gemm2(t, (const uint8_t*)gemm2_weights, gemm2_weights_scale, L, ws, output, stream);

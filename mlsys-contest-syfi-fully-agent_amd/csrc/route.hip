@@ -24,7 +24,7 @@
 //   * ranks inside a chunk come from wave ballots, so rows of an expert are in
 //     ascending token order and the result is deterministic; no host round
 //     trip at any T.
-#include "moe_common.hpp"
+#include "route_token.hpp"
 
 namespace moe {
 namespace {
@@ -33,140 +33,6 @@ constexpr int kRouteWaves = 16;      // tokens per route workgroup, T <= 16 (sin
 constexpr int kRouteWavesMulti = 4;  // tokens per route workgroup, 16 < T <= kRouteMultiSmallMaxTokens
 constexpr int kRouteMultiSmallMaxTokens = 1024;
 constexpr int kRouteThreads = kRouteWaves * kWave;
-
-// Maxima of the two half-waves (lanes 0-31, 32-63) of a 32-bit key,
-// wave-uniform.  Four DPP row steps, then rows 1 and 3 take rows 0 and 2.
-// Maximum over the wave, wave-uniform: DPP maxima within each row of 16
-// (bound_ctrl moves, which the compiler folds into v_max_u32_dpp), then the
-// four row maxima.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
-  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppQuad1032, 0xF, 0xF, true));
-  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppQuad2301, 0xF, 0xF, true));
-  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppRowHalfMirror, 0xF, 0xF, true));
-  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppRowMirror, 0xF, 0xF, true));
-  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)k, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
-  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)k, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
-  return max(max(a, b), max(c, d));
-}
-
-__device__ __forceinline__ void halfwave_max(uint32_t k, uint32_t& m0, uint32_t& m1) {
-  k = row16_max_u32(k);
-  k = max(k, dpp_u32<kDppRowBcast15, 0xA>(k));
-  m0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 31);
-  m1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
-}
-
-// Routes token t with one wavefront.  Returns the 8 selected ids, ascending
-// (wave-uniform), and their weights (wave-uniform).
-//
-// Lane l holds experts l, l+64, l+128, l+192 (slot j = expert / 64); the
-// routing group of 32 experts g = 2j + (l >= 32) is one half-wave of one slot.
-// Scores are compared through 32-bit order-preserving keys of the fp32 values
-// (masked experts: key 0, below every real score); among equal scores the
-// lower expert index wins.
-__device__ void route_token(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
-                            float rsf, int t, int sel[kTopK], float wsel[kTopK]) {
-  const int lane = threadIdx.x & (kWave - 1);
-  float s[4];
-  uint32_t key[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = 64 * j + lane;
-    const float x = logits[(size_t)t * kEGlobal + e];
-    // moe.py:127: s = 1/(1+exp(-x)); exp evaluated in double, rounded once.
-    const float ex = (float)exp(-(double)x);
-    s[j] = 1.0f / (1.0f + ex);
-    // moe.py:128: s_with_bias = s + bias
-    key[j] = float_order_key(s[j] + bf16_to_f32(bias[e]));
-  }
-  // moe.py:135-136: group score = sum of the two largest biased scores (a
-  // repeated maximum counts twice).  The four slots reduce independently.
-  float G[kNGroup];
-  uint32_t m1[4][2], m2[4][2];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) halfwave_max(key[j], m1[j][0], m1[j][1]);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t mine = lane < 32 ? m1[j][0] : m1[j][1];
-    const uint64_t eq = __ballot(key[j] == mine);
-    // drop one instance of the maximum (the lowest lane holding it)
-    const int lo0 = __builtin_ctzll(eq & 0x00000000FFFFFFFFull);
-    const int lo1 = __builtin_ctzll(eq & 0xFFFFFFFF00000000ull);
-    halfwave_max(lane == lo0 || lane == lo1 ? 0u : key[j], m2[j][0], m2[j][1]);
-    G[2 * j] = float_from_order_key(m1[j][0]) + float_from_order_key(m2[j][0]);
-    G[2 * j + 1] = float_from_order_key(m1[j][1]) + float_from_order_key(m2[j][1]);
-  }
-  // moe.py:139-146: keep the top-4 groups (ties -> lower group index).
-  uint32_t keep = 0;
-#pragma unroll
-  for (int g = 0; g < kNGroup; ++g) {
-    int rank = 0;
-#pragma unroll
-    for (int h = 0; h < kNGroup; ++h) rank += (G[h] > G[g]) || (G[h] == G[g] && h < g);
-    keep |= (rank < kTopKGroup ? 1u : 0u) << g;
-  }
-  // moe.py:149-151: top-8 experts among the kept groups, as eight rounds of
-  // (wave maximum of the keys, the lowest expert index holding it); the
-  // expert taken leaves the round's candidates.  This is the set "every key
-  // above the 8th largest, then the lowest indices among the keys equal to
-  // it" (keys of dropped groups are 0, below every real score).
-  const int half = lane >> 5;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (!((keep >> (2 * j + half)) & 1u)) key[j] = 0u;
-  uint32_t taken = 0u;  // bit j: this lane's expert 64j + lane already taken
-  int pick[kTopK];
-#pragma unroll
-  for (int r = 0; r < kTopK; ++r) {
-    const uint32_t M = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
-    // slot j: lanes holding M (taken experts hold 0, so only a zero maximum
-    // needs the taken bits)
-    uint64_t b[4];
-    if (M != 0u) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = __ballot(key[j] == M);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = __ballot(key[j] == 0u && !((taken >> j) & 1u));
-    }
-    // lowest expert index 64j + lane among them
-    int t = 4 * kWave;
-#pragma unroll
-    for (int j = 3; j >= 0; --j)
-      if (b[j]) t = 64 * j + __builtin_ctzll(b[j]);
-    pick[r] = t;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (64 * j + lane == t) {
-        key[j] = 0u;
-        taken |= 1u << j;
-      }
-  }
-  // ids ascending: Batcher's 19-comparator network on the (wave-uniform) ids
-  constexpr int kNet[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
-                               {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
-#pragma unroll
-  for (int c = 0; c < 19; ++c) {
-    const int x = pick[kNet[c][0]], y = pick[kNet[c][1]];
-    pick[kNet[c][0]] = min(x, y);
-    pick[kNet[c][1]] = max(x, y);
-  }
-#pragma unroll
-  for (int r = 0; r < kTopK; ++r) {
-    const int j = pick[r] >> 6, l = pick[r] & 63;
-    sel[r] = pick[r];
-    const float sj = j == 0 ? s[0] : j == 1 ? s[1] : j == 2 ? s[2] : s[3];
-    wsel[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), l));
-  }
-  // moe.py:154-158: weights from the un-biased sigmoid, summed in ascending id
-  // order, normalised (true division) then scaled.
-  float sum = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kTopK; ++k) sum = sum + wsel[k];
-  const float denom = sum + 1e-20f;
-#pragma unroll
-  for (int k = 0; k < kTopK; ++k) wsel[k] = (wsel[k] / denom) * rsf;
-}
 
 // Local-expert bitmask of a token's 8 ascending ids, and the slot of its first
 // local id (ids ascending => local ids occupy slots kfirst .. kfirst+popc-1).
@@ -279,12 +145,9 @@ __device__ void scatter_chunk(const int32_t* __restrict__ ids, const float* __re
   __syncthreads();  // wave_cnt / wave_base may be reused
 }
 
-// Routing of 16 tokens per workgroup.  With a single workgroup (T <= 16) it
-// also builds the permutation, from LDS only (no global round trip of the
-// ids); otherwise it writes its local-expert histogram to
-// block_hist[blockIdx.x][32] for perm_kernel.
 // kW tokens per workgroup, one wave each.  kSingle (T <= 16): one workgroup
-// of 16 waves also builds the permutation.  Otherwise every workgroup writes
+// of 16 waves also builds the permutation (route_small).  Otherwise every
+// workgroup writes
 // its per-expert counts to block_hist for perm_kernel.  Up to
 // kRouteMultiSmallMaxTokens tokens the workgroups have 4 waves (one wave per
 // SIMD: the routing chain of a token is a long run of dependent wave-level
@@ -297,15 +160,15 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
              int32_t* __restrict__ pair_row, int32_t* __restrict__ expert_off,
              int32_t* __restrict__ perm_token, float* __restrict__ perm_w, int32_t* __restrict__ block_hist) {
   static_assert(kW == kRouteWaves || (kW == kRouteWavesMulti && !kSingle), "route workgroup shapes");
-  __shared__ int hist[kELocal];
-  __shared__ uint32_t tokmask[kELocal];  // bit w: this workgroup's token w chose local expert
-  __shared__ int first_row[kELocal];
-  __shared__ int pair_id[kW][kTopK];
-  __shared__ float pair_w[kW][kTopK];
-  if (threadIdx.x < kELocal) {
-    hist[threadIdx.x] = 0;
-    tokmask[threadIdx.x] = 0u;
+  if constexpr (kSingle) {
+    static_assert(kW == kSmallRouteMaxTokens, "one wave per token");
+    __shared__ SmallRoute sr;
+    const RouteOut out{ids, w, pair_row, expert_off, perm_token, perm_w};
+    route_small(logits, bias, rsf, T, offset, sr, out, true);
+    return;
   }
+  __shared__ int hist[kELocal];
+  if (threadIdx.x < kELocal) hist[threadIdx.x] = 0;
   __syncthreads();
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -326,49 +189,12 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
         }
       ids[(size_t)t * kTopK + lane] = e;
       w[(size_t)t * kTopK + lane] = we;
-      pair_id[tw][lane] = e;
-      pair_w[tw][lane] = we;
       const int64_t le = (int64_t)e - offset;
-      if (le >= 0 && le < kELocal) {
-        atomicAdd(&hist[(int)le], 1);
-        atomicOr(&tokmask[(int)le], 1u << tw);
-      }
+      if (le >= 0 && le < kELocal) atomicAdd(&hist[(int)le], 1);
     }
   }
   __syncthreads();
-  if (!kSingle) {
-    if (threadIdx.x < kELocal) block_hist[(size_t)blockIdx.x * kELocal + threadIdx.x] = hist[threadIdx.x];
-    return;
-  }
-  // T <= 16: rows of expert le are its tokens in ascending order, starting at
-  // the exclusive scan of the per-expert counts.
-  if (threadIdx.x < kWave) {
-    const int c = lane < kELocal ? __popc(tokmask[lane]) : 0;
-    int incl = c;
-#pragma unroll
-    for (int d = 1; d < kELocal; d <<= 1) {
-      const int v = __shfl_up(incl, d, kWave);
-      if (lane >= d) incl += v;
-    }
-    if (lane < kELocal) {
-      first_row[lane] = incl - c;
-      expert_off[lane] = incl - c;
-      if (lane == kELocal - 1) expert_off[kELocal] = incl;
-    }
-  }
-  __syncthreads();
-  const int p = threadIdx.x;  // pair p = (token p / 8, slot p % 8)
-  if (p < T * kTopK) {
-    const int pt = p / kTopK, k = p % kTopK;
-    const int64_t le = (int64_t)pair_id[pt][k] - offset;
-    int row = -1;
-    if (le >= 0 && le < kELocal) {
-      row = first_row[le] + __popc(tokmask[le] & ((1u << pt) - 1u));
-      perm_token[row] = pt;
-      perm_w[row] = pair_w[pt][k];
-    }
-    pair_row[p] = row;
-  }
+  if (threadIdx.x < kELocal) block_hist[(size_t)blockIdx.x * kELocal + threadIdx.x] = hist[threadIdx.x];
 }
 
 // Permutation for T > 16: workgroup c handles tokens [1024c, 1024c + 1024).

@@ -1,0 +1,241 @@
+// route_token.hpp -- DeepSeek-V3 grouped routing of one token by one
+// wavefront (moe.py:123-158), and the whole routing with the permutation for
+// up to 16 tokens in one workgroup (moe.py:168-179).  Used by the routing
+// kernels and by GEMM1's decode path, which routes its few tokens itself
+// instead of waiting for a routing launch.
+#pragma once
+
+#include "moe_common.hpp"
+
+namespace moe {
+
+// Maximum over the wave, wave-uniform: DPP maxima within each row of 16
+// (bound_ctrl moves, which the compiler folds into v_max_u32_dpp), then the
+// four row maxima.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
+  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppQuad1032, 0xF, 0xF, true));
+  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppQuad2301, 0xF, 0xF, true));
+  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppRowHalfMirror, 0xF, 0xF, true));
+  k = max(k, (uint32_t)__builtin_amdgcn_mov_dpp((int)k, kDppRowMirror, 0xF, 0xF, true));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)k, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)k, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
+  return max(max(a, b), max(c, d));
+}
+
+// Maxima of the two half-waves (lanes 0-31, 32-63) of a 32-bit key,
+// wave-uniform.  Four DPP row steps, then rows 1 and 3 take rows 0 and 2.
+__device__ __forceinline__ void halfwave_max(uint32_t k, uint32_t& m0, uint32_t& m1) {
+  k = row16_max_u32(k);
+  k = max(k, dpp_u32<kDppRowBcast15, 0xA>(k));
+  m0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 31);
+  m1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
+}
+
+// Routes token t with one wavefront.  Returns the 8 selected ids, ascending
+// (wave-uniform), and their weights (wave-uniform).
+//
+// Lane l holds experts l, l+64, l+128, l+192 (slot j = expert / 64); the
+// routing group of 32 experts g = 2j + (l >= 32) is one half-wave of one slot.
+// Scores are compared through 32-bit order-preserving keys of the fp32 values
+// (masked experts: key 0, below every real score); among equal scores the
+// lower expert index wins.
+__device__ inline void route_token(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
+                            float rsf, int t, int sel[kTopK], float wsel[kTopK]) {
+  const int lane = threadIdx.x & (kWave - 1);
+  float s[4];
+  uint32_t key[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 64 * j + lane;
+    const float x = logits[(size_t)t * kEGlobal + e];
+    // moe.py:127: s = 1/(1+exp(-x)); exp evaluated in double, rounded once.
+    const float ex = (float)exp(-(double)x);
+    s[j] = 1.0f / (1.0f + ex);
+    // moe.py:128: s_with_bias = s + bias
+    key[j] = float_order_key(s[j] + bf16_to_f32(bias[e]));
+  }
+  // moe.py:135-136: group score = sum of the two largest biased scores (a
+  // repeated maximum counts twice).  The four slots reduce independently.
+  float G[kNGroup];
+  uint32_t m1[4][2], m2[4][2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) halfwave_max(key[j], m1[j][0], m1[j][1]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t mine = lane < 32 ? m1[j][0] : m1[j][1];
+    const uint64_t eq = __ballot(key[j] == mine);
+    // drop one instance of the maximum (the lowest lane holding it)
+    const int lo0 = __builtin_ctzll(eq & 0x00000000FFFFFFFFull);
+    const int lo1 = __builtin_ctzll(eq & 0xFFFFFFFF00000000ull);
+    halfwave_max(lane == lo0 || lane == lo1 ? 0u : key[j], m2[j][0], m2[j][1]);
+    G[2 * j] = float_from_order_key(m1[j][0]) + float_from_order_key(m2[j][0]);
+    G[2 * j + 1] = float_from_order_key(m1[j][1]) + float_from_order_key(m2[j][1]);
+  }
+  // moe.py:139-146: keep the top-4 groups (ties -> lower group index).
+  uint32_t keep = 0;
+#pragma unroll
+  for (int g = 0; g < kNGroup; ++g) {
+    int rank = 0;
+#pragma unroll
+    for (int h = 0; h < kNGroup; ++h) rank += (G[h] > G[g]) || (G[h] == G[g] && h < g);
+    keep |= (rank < kTopKGroup ? 1u : 0u) << g;
+  }
+  // moe.py:149-151: top-8 experts among the kept groups, as eight rounds of
+  // (wave maximum of the keys, the lowest expert index holding it); the
+  // expert taken leaves the round's candidates.  This is the set "every key
+  // above the 8th largest, then the lowest indices among the keys equal to
+  // it" (keys of dropped groups are 0, below every real score).
+  const int half = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (!((keep >> (2 * j + half)) & 1u)) key[j] = 0u;
+  uint32_t taken = 0u;  // bit j: this lane's expert 64j + lane already taken
+  int pick[kTopK];
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    const uint32_t M = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+    // slot j: lanes holding M (taken experts hold 0, so only a zero maximum
+    // needs the taken bits)
+    uint64_t b[4];
+    if (M != 0u) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = __ballot(key[j] == M);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = __ballot(key[j] == 0u && !((taken >> j) & 1u));
+    }
+    // lowest expert index 64j + lane among them
+    int t = 4 * kWave;
+#pragma unroll
+    for (int j = 3; j >= 0; --j)
+      if (b[j]) t = 64 * j + __builtin_ctzll(b[j]);
+    pick[r] = t;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (64 * j + lane == t) {
+        key[j] = 0u;
+        taken |= 1u << j;
+      }
+  }
+  // ids ascending: Batcher's 19-comparator network on the (wave-uniform) ids
+  constexpr int kNet[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
+                               {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+  for (int c = 0; c < 19; ++c) {
+    const int x = pick[kNet[c][0]], y = pick[kNet[c][1]];
+    pick[kNet[c][0]] = min(x, y);
+    pick[kNet[c][1]] = max(x, y);
+  }
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) {
+    const int j = pick[r] >> 6, l = pick[r] & 63;
+    sel[r] = pick[r];
+    const float sj = j == 0 ? s[0] : j == 1 ? s[1] : j == 2 ? s[2] : s[3];
+    wsel[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), l));
+  }
+  // moe.py:154-158: weights from the un-biased sigmoid, summed in ascending id
+  // order, normalised (true division) then scaled.
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) sum = sum + wsel[k];
+  const float denom = sum + 1e-20f;
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) wsel[k] = (wsel[k] / denom) * rsf;
+}
+
+// ---------------------------------------------------------------------------
+// Routing and permutation of T <= 16 tokens in one workgroup, from LDS only
+// (no global round trip of the ids).  Token t is routed by wave t % waves.
+// Rows of local expert le are its tokens in ascending order (moe.py:168-179),
+// starting at the exclusive scan of the per-expert counts.  `sr` is LDS of
+// the caller (inside its single LDS object); the workspace outputs `out`
+// are written only when `write_out` is set.
+// ---------------------------------------------------------------------------
+constexpr int kSmallRouteMaxTokens = 16;
+
+struct SmallRoute {
+  uint32_t tokmask[kELocal];                       // bit t: token t chose local expert le
+  int expert_off[kELocal + 1];                     // first row per local expert; [32] = rows
+  int pair_id[kSmallRouteMaxTokens][kTopK];        // selected global ids, ascending
+  float pair_w[kSmallRouteMaxTokens][kTopK];       // their weights
+  int perm_token[kSmallRouteMaxTokens * kTopK];    // token of each permuted row
+  float perm_w[kSmallRouteMaxTokens * kTopK];      // weight of each permuted row
+};
+
+struct RouteOut {
+  int32_t* ids;
+  float* w;
+  int32_t* pair_row;
+  int32_t* expert_off;
+  int32_t* perm_token;
+  float* perm_w;
+};
+
+__device__ inline void route_small(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf,
+                                   int T, int64_t offset, SmallRoute& sr, RouteOut out, bool write_out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int waves = blockDim.x / kWave;
+  if (threadIdx.x < kELocal) sr.tokmask[threadIdx.x] = 0u;
+  __syncthreads();
+  for (int t = wave; t < T; t += waves) {
+    int sel[kTopK];
+    float wsel[kTopK];
+    route_token(logits, bias, rsf, t, sel, wsel);
+    if (lane < kTopK) {
+      int e = sel[0];
+      float we = wsel[0];
+#pragma unroll
+      for (int r = 1; r < kTopK; ++r)
+        if (lane == r) {
+          e = sel[r];
+          we = wsel[r];
+        }
+      if (write_out) {
+        out.ids[(size_t)t * kTopK + lane] = e;
+        out.w[(size_t)t * kTopK + lane] = we;
+      }
+      sr.pair_id[t][lane] = e;
+      sr.pair_w[t][lane] = we;
+      const int64_t le = (int64_t)e - offset;
+      if (le >= 0 && le < kELocal) atomicOr(&sr.tokmask[(int)le], 1u << t);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    const int c = lane < kELocal ? __popc(sr.tokmask[lane]) : 0;
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < kELocal; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += v;
+    }
+    if (lane < kELocal) {
+      sr.expert_off[lane] = incl - c;
+      if (write_out) out.expert_off[lane] = incl - c;
+      if (lane == kELocal - 1) {
+        sr.expert_off[kELocal] = incl;
+        if (write_out) out.expert_off[kELocal] = incl;
+      }
+    }
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < T * kTopK; p += blockDim.x) {  // pair p = (token p / 8, slot p % 8)
+    const int pt = p / kTopK, k = p % kTopK;
+    const int64_t le = (int64_t)sr.pair_id[pt][k] - offset;
+    int row = -1;
+    if (le >= 0 && le < kELocal) {
+      row = sr.expert_off[le] + __popc(sr.tokmask[le] & ((1u << pt) - 1u));
+      sr.perm_token[row] = pt;
+      sr.perm_w[row] = sr.pair_w[pt][k];
+      if (write_out) {
+        out.perm_token[row] = pt;
+        out.perm_w[row] = sr.pair_w[pt][k];
+      }
+    }
+    if (write_out) out.pair_row[p] = row;
+  }
+  __syncthreads();
+}
+
+}  // namespace moe
