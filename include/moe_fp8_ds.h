@@ -80,7 +80,8 @@ int moe_fp8_ds_run(const float* routing_logits, const void* routing_bias,
                    int64_t T, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Number of device stages of moe_fp8_ds_run: routing + permutation, GEMM1 +
- * SwiGLU, GEMM2, combine. */
+ * SwiGLU, GEMM2, combine.  For T <= 16 the routing runs inside GEMM1 (stage 0
+ * is empty), and for T <= 64 the combine inside GEMM2 (stage 3 is empty). */
 #define MOE_FP8_DS_NUM_STAGES 4
 
 /* moe_fp8_ds_run, plus a hipEventRecord on `stream` before the first stage and
