@@ -22,9 +22,11 @@ namespace {
 // ---------------------------------------------------------------------------
 // Streaming path with the combine fused in (T <= kGemm2StreamMaxTokens).
 //
-//   * a workgroup owns 16 output columns n0..n0+15 for all T tokens; it walks
+//   * a workgroup owns 32 output columns n0..n0+31 for all T tokens; it walks
 //     the active experts in ascending order (the order of moe.py:168-200) and
-//     their 16-row tiles, computing O = act_rows . W2_e[n0..n0+15]^T;
+//     their 16-row tiles, computing O = act_rows . W2_e[n0..n0+31]^T
+//     (two 16-column MFMA blocks: each job's act rows are loaded once for
+//     32 columns, which halves their L2 traffic against 16-column groups);
 //   * its 8 waves split K (2 scale blocks each); the loads of the next
 //     (expert, row tile) job are issued before the current one is multiplied;
 //   * the K-partials are summed in LDS in a fixed order and each row's
@@ -32,14 +34,17 @@ namespace {
 //     (acc = acc + O * w, the two roundings of moe.py:199-200); a token occurs
 //     at most once per expert, so no atomics are needed and the result is
 //     deterministic;
-//   * finally every token's 16 columns are rounded to bf16 and stored (tokens
+//   * finally every token's 32 columns are rounded to bf16 and stored (tokens
 //     without a local expert get zeros).  No GEMM2 rows reach HBM and no
 //     separate combine pass runs.
 // ---------------------------------------------------------------------------
 constexpr int kS2Waves = 8;
 constexpr int kS2Threads = kS2Waves * kWave;
 constexpr int kS2KB = kNIBlk / kS2Waves;  // 2 scale blocks per wave
-constexpr int kS2Units = kH / 16;         // 448 column groups
+constexpr int kS2NB = 2;                  // 16-column blocks per workgroup
+constexpr int kS2Cols = 16 * kS2NB;       // output columns per workgroup
+constexpr int kS2Units = kH / kS2Cols;    // 224 column groups
+static_assert(kBlk % kS2Cols == 0, "a workgroup's columns share one weight scale block");
 
 struct S2Job {
   int e, rt;  // expert, row tile; e < 0: none
@@ -56,7 +61,7 @@ struct S2Regs {
   v4i a[kS2KB][2][2];  // bf16 act: elements 64g + 16q + 8h .. +7
   float sw[kS2KB];
   int tok;           // token and weight of the row this thread combines
-  float pw;          //   (threads < 256: row = tid / 16 of the tile)
+  float pw;          //   (row = (tid / 16) % 16 of the tile)
 };
 
 __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
@@ -80,20 +85,22 @@ __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
   }
 }
 
-// A job's W2 bytes of this wave (16 rows n0.., K blocks kb0, kb0 + 1) -> the
-// wave's LDS stage: per K block two wide planes (rows 0-7, 8-15), 128 bytes
-// per row, chunks swizzled, so every copy reads 8 whole 128-byte row
-// segments.  4 copies per lane.
+// A job's W2 bytes of this wave (rows n0 .. n0 + 31, K blocks kb0, kb0 + 1)
+// -> the wave's LDS stage: per 16-row block and K block two wide planes (rows
+// 0-7, 8-15), 128 bytes per row, chunks swizzled, so every copy reads 8 whole
+// 128-byte row segments.  8 copies per lane.
 __device__ __forceinline__ void s2_copy_w(char* stage, S2Job j, const uint8_t* __restrict__ w2, int n0, int kb0,
                                           int lane) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    int r, c;
-    wide_copy_lane(lane, h, r, c);
-    const uint8_t* src = w2 + ((size_t)j.e * kH + n0 + r) * kI + kb0 * kBlk + 16 * c;
+  for (int nb = 0; nb < kS2NB; ++nb)
 #pragma unroll
-    for (int k = 0; k < kS2KB; ++k) dma16(src + k * kBlk, stage + (2 * k + h) * 1024);
-  }
+    for (int h = 0; h < 2; ++h) {
+      int r, c;
+      wide_copy_lane(lane, h, r, c);
+      const uint8_t* src = w2 + ((size_t)j.e * kH + n0 + 16 * nb + r) * kI + kb0 * kBlk + 16 * c;
+#pragma unroll
+      for (int k = 0; k < kS2KB; ++k) dma16(src + k * kBlk, stage + ((nb * kS2KB + k) * 2 + h) * 1024);
+    }
 }
 
 __global__ void __launch_bounds__(kS2Threads)
@@ -104,22 +111,22 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
   // One LDS object (a second __shared__ array makes the compiler wait for
   // every LDS DMA before any LDS read): per wave a two-stage W2 ring, then
   // the token accumulators and the K-partials.
-  constexpr int kStage = kS2KB * 2 * 1024;                 // 4 KB per wave and job
+  constexpr int kStage = kS2NB * kS2KB * 2 * 1024;         // 8 KB per wave and job
   constexpr int kRing = 2 * kS2Waves * kStage;
   constexpr int kAccOff = kRing;
-  constexpr int kRedOff = kAccOff + kGemm2StreamMaxTokens * 16 * 4;
-  constexpr int kLdsBytes = kRedOff + kS2Waves * 256 * 4;
+  constexpr int kRedOff = kAccOff + kGemm2StreamMaxTokens * kS2Cols * 4;
+  constexpr int kLdsBytes = kRedOff + kS2Waves * kS2NB * 256 * 4;
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
-  float* outacc = (float*)(lds + kAccOff);  // [token][16]
-  float* red = (float*)(lds + kRedOff);     // [wave][256]
-  const int n0 = blockIdx.x * 16;
+  float* outacc = (float*)(lds + kAccOff);  // [token][32]
+  float* red = (float*)(lds + kRedOff);     // [wave][column block][256]
+  const int n0 = blockIdx.x * kS2Cols;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x & (kWave - 1);
   const int lq = lane >> 4;
   const int lr = lane & 15;
   const int kb0 = wave * kS2KB;
   auto stage = [&](int s) { return lds + (s * kS2Waves + wave) * kStage; };
-  for (int i = threadIdx.x; i < T * 16; i += kS2Threads) outacc[i] = 0.f;
+  for (int i = threadIdx.x; i < T * kS2Cols; i += kS2Threads) outacc[i] = 0.f;
 
   ExpertRows X;
   X.load(expert_off);
@@ -140,47 +147,56 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
   // Issue order is always: act rows of job j, copy of job j + 1.
   auto step = [&](int s, const S2Regs& cur, S2Regs& nxt) {
     // This job's W2 stage and act rows have landed; the next job's W2 copy
-    // (4 per lane, issued last) may stay in flight.
+    // (8 per lane, issued last) may stay in flight.
     if (j1.e >= 0)
-      wait_vmcnt_lgkm0<2 * kS2KB>();
+      wait_vmcnt_lgkm0<2 * kS2KB * kS2NB>();
     else
       wait_vmcnt_lgkm0<0>();
     asm volatile("" ::: "memory");
-    v4i b[kS2KB][2];
+    v4i b[kS2NB][kS2KB][2];
 #pragma unroll
-    for (int k = 0; k < kS2KB; ++k)
+    for (int nb = 0; nb < kS2NB; ++nb)
 #pragma unroll
-      for (int g = 0; g < 2; ++g) b[k][g] = *(const v4i*)(stage(s) + 2 * k * 1024 + wide_slot(lr, 4 * g + lq));
+      for (int k = 0; k < kS2KB; ++k)
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+          b[nb][k][g] = *(const v4i*)(stage(s) + 2 * (nb * kS2KB + k) * 1024 + wide_slot(lr, 4 * g + lq));
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the stage is read: free for the job after next
     const S2Job j2 = j1.e >= 0 ? s2_next(X, active, j1) : j1;
     if (j1.e >= 0) s2_load(nxt, j1, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
     if (j2.e >= 0) s2_copy_w(stage(s), j2, w2, n0, kb0, lane);
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < kS2KB; ++k) {
-      v4f p = {0.f, 0.f, 0.f, 0.f};
+    for (int nb = 0; nb < kS2NB; ++nb) {
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][0]),
-                               e4m3x8_to_bf16((uint32_t)b[k][g][0], (uint32_t)b[k][g][1]), p);
-        p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][1]),
-                               e4m3x8_to_bf16((uint32_t)b[k][g][2], (uint32_t)b[k][g][3]), p);
+      for (int k = 0; k < kS2KB; ++k) {
+        v4f p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][0]),
+                                 e4m3x8_to_bf16((uint32_t)b[nb][k][g][0], (uint32_t)b[nb][k][g][1]), p);
+          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][1]),
+                                 e4m3x8_to_bf16((uint32_t)b[nb][k][g][2], (uint32_t)b[nb][k][g][3]), p);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], cur.sw[k], acc[i]);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], cur.sw[k], acc[i]);
+      for (int i = 0; i < 4; ++i) red[(wave * kS2NB + nb) * 256 + (4 * lq + i) * 16 + lr] = acc[i];
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[wave * 256 + (4 * lq + i) * 16 + lr] = acc[i];
     lds_barrier();
-    if (threadIdx.x < 256) {
-      const int r = threadIdx.x >> 4, c = threadIdx.x & 15;
+    {
+      // thread = (column block nb, row r, column c): every thread of the workgroup
+      static_assert(kS2Threads == kS2NB * 256, "one thread per output of a job");
+      const int nb = threadIdx.x >> 8, r = (threadIdx.x >> 4) & 15, c = threadIdx.x & 15;
       const int row = X.begin(job.e) + job.rt * 16 + r;
       if (row < X.end(job.e)) {
-        float o = red[threadIdx.x];
+        float o = red[nb * 256 + (threadIdx.x & 255)];
 #pragma unroll
-        for (int w = 1; w < kS2Waves; ++w) o += red[w * 256 + threadIdx.x];
+        for (int w = 1; w < kS2Waves; ++w) o += red[(w * kS2NB + nb) * 256 + (threadIdx.x & 255)];
         const float p = o * cur.pw;
-        outacc[cur.tok * 16 + c] = outacc[cur.tok * 16 + c] + p;
+        float& a = outacc[cur.tok * kS2Cols + 16 * nb + c];
+        a = a + p;
       }
     }
     lds_barrier();
@@ -193,8 +209,8 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
     if (job.e < 0) break;
     step(1, r1, r0);
   }
-  for (int i = threadIdx.x; i < T * 16; i += kS2Threads)
-    out[(size_t)(i >> 4) * kH + n0 + (i & 15)] = f32_to_bf16_rne(outacc[i]);
+  for (int i = threadIdx.x; i < T * kS2Cols; i += kS2Threads)
+    out[(size_t)(i / kS2Cols) * kH + n0 + (i % kS2Cols)] = f32_to_bf16_rne(outacc[i]);
 }
 
 // ---------------------------------------------------------------------------
