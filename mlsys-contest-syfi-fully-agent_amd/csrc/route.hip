@@ -16,7 +16,9 @@
 //     expert holding it, the ids then sorted by a comparator network;
 //   * T <= 16 (decode): the single workgroup also builds the permutation from
 //     LDS (per-expert token bitmasks), with no global atomics, fences or
-//     re-reads of the ids;
+//     re-reads of the ids (route_small, route_token.hpp).  The layer itself
+//     runs that routing inside GEMM1 for T <= 16; this kernel serves the
+//     routing-only entry point there;
 //   * larger T: each workgroup stores its local-expert histogram (plain
 //     stores, no atomics); a second kernel (one workgroup per 1024 tokens)
 //     reduces the histograms to the expert row offsets and the per-chunk bases
