@@ -47,6 +47,9 @@ constexpr int kS1Waves = 8;
 constexpr int kS1Threads = kS1Waves * kWave;
 constexpr int kS1KB = kNHBlk / kS1Waves;  // 7 scale blocks per wave
 constexpr int kS1Groups = kI / 8;         // 256 column groups per expert
+constexpr int kS1CopySplit = 4;           // weight copy parts: K blocks [0, 4) and [4, 7)
+constexpr int kS1CopyOps0 = 2 * kS1CopySplit;            // copies per lane, part 0
+constexpr int kS1CopyOps1 = 2 * (kS1KB - kS1CopySplit);  // copies per lane, part 1
 
 // Operands of one 16-row tile that go out before it is multiplied.
 struct S1TileOps {
@@ -139,7 +142,10 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
   // instruction reads 8 whole 128-byte row segments (the fast lane order for
   // the vector memory path) and the fragment reads are free of bank
   // conflicts.
-  auto copy_w = [&](int item) {
+  // Copied in two parts so that the next item's copy can start before this
+  // item's second part has landed: part 0 = K blocks 0-3 (8 copies per lane),
+  // part 1 = K blocks 4-6 (6 copies per lane).
+  auto copy_w = [&](int item, int part) {
     const int cg = item % kS1Groups;
     const int e = nth_set_bit(active, item / kS1Groups);
 #pragma unroll
@@ -149,7 +155,8 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
       const size_t n = (size_t)e * k2I + (r < 8 ? 8 * cg + r : kI + 8 * cg + (r - 8));
       const uint8_t* src = w13 + n * kH + kb0 * kBlk + 16 * c;
 #pragma unroll
-      for (int j = 0; j < kS1KB; ++j) dma16(src + j * kBlk, wbuf + (2 * j + h) * 1024);
+      for (int j = 0; j < kS1KB; ++j)
+        if ((j < kS1CopySplit) == (part == 0)) dma16(src + j * kBlk, wbuf + (2 * j + h) * 1024);
     }
   };
   // Row tile rt of an item: token of this lane's A row (kDirect: the rows
@@ -168,11 +175,19 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     o.ptok = 0;
     if (kDirect && (int)threadIdx.x < X.end(e) - X.begin(e)) o.ptok = ptok_src[X.begin(e) + threadIdx.x];
   };
-  // The item's weight block scales (this lane's column).
+  // The item's weight block scales (this lane's column): the gate rows and
+  // the up rows of an item lie in one 128-row scale block each, so the loads
+  // are wave-uniform (scalar loads, counted by lgkmcnt, not vmcnt).
   auto issue_sw = [&](int item, S1TileOps& o) {
-    const float* sp = w13_scale + (w_row(item) / kBlk) * kNHBlk + kb0;
+    const int cg = item % kS1Groups;
+    const int e = nth_set_bit(active, item / kS1Groups);
+    const float* sg = w13_scale + (((size_t)e * k2I + 8 * cg) / kBlk) * kNHBlk + kb0;
+    const float* su = w13_scale + (((size_t)e * k2I + kI + 8 * cg) / kBlk) * kNHBlk + kb0;
 #pragma unroll
-    for (int j = 0; j < kS1KB; ++j) o.sw[j] = sp[j];
+    for (int j = 0; j < kS1KB; ++j) {
+      const float g = sg[j], u = su[j];
+      o.sw[j] = lr < 8 ? g : u;
+    }
   };
   // Multiply a landed tile, reduce the 8 K-partials in a fixed order, SwiGLU,
   // store the activation rows.
@@ -235,30 +250,52 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
   S1TileOps cur;
   S1Out pend;       // the previous tile's outputs, stored once the next loads are out
   if (i0 < i1) {
-    copy_w(i0);
     issue_rows(i0, 0, cur);
     issue_sw(i0, cur);
+    copy_w(i0, 0);
+    copy_w(i0, 1);
   }
+  // fragment of block j: lane (q, r) holds row r, K bytes 32q .. 32q+31
+  const int slot_lo = wide_slot(lr, 2 * lq), slot_hi = wide_slot(lr, 2 * lq + 1);
+  auto read_b = [&](v8i (&b)[kS1KB], int j) {
+    const v4i lo = *(const v4i*)(wbuf + 2 * j * 1024 + slot_lo);
+    const v4i hi = *(const v4i*)(wbuf + 2 * j * 1024 + slot_hi);
+    b[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+  // Vector-memory order per item: [row operands, only when the expert
+  // changes] [copy part 0] ... [copy part 1] [the previous tile's store].
+  // The weight scales are scalar loads (lgkmcnt), so outside an expert change
+  // only copies and at most one store are counted.
 #pragma unroll 1
   for (int item = i0; item < i1; ++item) {
-    wait_vmcnt_lgkm0<0>();
+    const bool more = item + 1 < i1;
+    const bool new_rows = more && (item + 1) / kS1Groups != item / kS1Groups;
+    // Part 0 has landed, and the row operands issued before it; part 1 and
+    // the store after it may still be in flight.
+    wait_vmcnt_lgkm0<kS1CopyOps1>();
     asm volatile("" ::: "memory");
-    // fragment of block j: lane (q, r) holds row r, K bytes 32q .. 32q+31
     v8i b[kS1KB];
-    const int slot_lo = wide_slot(lr, 2 * lq), slot_hi = wide_slot(lr, 2 * lq + 1);
 #pragma unroll
-    for (int j = 0; j < kS1KB; ++j) {
-      const v4i lo = *(const v4i*)(wbuf + 2 * j * 1024 + slot_lo);
-      const v4i hi = *(const v4i*)(wbuf + 2 * j * 1024 + slot_hi);
-      b[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the buffer is read: free for the next copy
+    for (int j = 0; j < kS1CopySplit; ++j) read_b(b, j);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // part 0 is read: free for the next item's
     S1TileOps nxt = cur;
-    if (item + 1 < i1) {
-      copy_w(item + 1);
-      if ((item + 1) / kS1Groups != item / kS1Groups) issue_rows(item + 1, 0, nxt);
+    if (more) {
       issue_sw(item + 1, nxt);
+      if (new_rows) issue_rows(item + 1, 0, nxt);
+      copy_w(item + 1, 0);
     }
+    // Part 1 has landed; the next item's part 0 may still be in flight (after
+    // new row operands, whose load count is not fixed, everything is waited
+    // for: once per expert change).
+    if (more && !new_rows)
+      wait_vmcnt_lgkm0<kS1CopyOps0>();
+    else
+      wait_vmcnt_lgkm0<0>();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int j = kS1CopySplit; j < kS1KB; ++j) read_b(b, j);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // part 1 is read
+    if (more) copy_w(item + 1, 1);
     if (item != i0) store_out(item - 1, pend);
     compute_tile(item, 0, cur, b, pend);
     if (!kDirect) {
