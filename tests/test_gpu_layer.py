@@ -178,3 +178,36 @@ def test_synth_matches_cpu_generator(pkg, orc, cuda_device):
     np.testing.assert_array_equal(w_host[1][:2], ref[1][:2])
     np.testing.assert_array_equal(w_host[2][:2], ref[2][:2])
     np.testing.assert_array_equal(w_host[3][:2], ref[3][:2])
+
+
+ROUTE_IN_GEMM1_CASES = [
+    ("decode_t1_s3", None, None),
+    ("plumbing_t16", None, None),
+    ("small_t64", None, 7),         # T < 8: some waves route no token
+    ("small_t64", 224, 16),         # last routing group local
+    ("prefill_t1024", 256, 5),      # no local expert at all
+]
+
+
+@pytest.mark.parametrize("name,offset,T", ROUTE_IN_GEMM1_CASES)
+def test_routing_inside_gemm1_matches_route_kernel(pkg, cuda_device, name, offset, T):
+    """T <= 16: the layer routes inside GEMM1 (every workgroup from LDS,
+    workgroup 0 writing the results); the workspace routing results equal the
+    routing-only entry point's bit for bit."""
+    cfg = pkg.synth.CONFIGS[name]
+    off = cfg.local_expert_offset if offset is None else offset
+    w, _ = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, _ = gpu_tokens(pkg, cfg, cuda_device, T)
+    T = tok[0].shape[0]
+    assert T <= 16
+    print(f"routing-in-GEMM1 case {name} offset={off} T={T}", flush=True)
+    run_layer(pkg, tok, w, off, cfg.routed_scaling_factor)
+    lay = pkg.intermediates(pkg.workspace(cuda_device, T), T)
+    n = int(lay.expert_off[32].item())
+    got = [x.clone() for x in (lay.topk_ids, lay.topk_w, lay.pair_row, lay.expert_off, lay.perm_token[:n], lay.perm_w[:n])]
+    ws = torch.empty_like(pkg.workspace(cuda_device, T))
+    r = pkg.route(tok[0], tok[1], off, cfg.routed_scaling_factor, ws=ws)
+    torch.cuda.synchronize()
+    exp = (r.topk_ids, r.topk_w, r.pair_row, r.expert_off, r.perm_token[:n], r.perm_w[:n])
+    for name_, g, e in zip(("ids", "w", "pair_row", "expert_off", "perm_token", "perm_w"), got, exp):
+        assert torch.equal(g, e), f"{name_} differs"
