@@ -17,7 +17,9 @@ namespace moe {
 namespace {
 
 // 448 threads x 16 columns = one 7168-column row per workgroup; every lane
-// issues its (up to 8 rows x 2) 16-byte loads before the first add.
+// issues its (up to 8 rows x 2) 16-byte loads before the first add.  Thread i
+// takes the 8-column chunks i and i + 448, so each load or store instruction
+// of a wave covers 1 KB of contiguous bytes.
 constexpr int kCombThreads = 448;
 constexpr int kCombCols = 16;
 static_assert(kCombThreads * kCombCols == kH, "one row per workgroup");
@@ -26,7 +28,7 @@ __global__ void __launch_bounds__(kCombThreads)
 combine_kernel(const uint16_t* __restrict__ down, const int32_t* __restrict__ pair_row,
                const float* __restrict__ topk_w, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
-  const int c = threadIdx.x * kCombCols;
+  const int c0 = threadIdx.x * 8, c1 = (threadIdx.x + kCombThreads) * 8;  // chunk h starts at column c_h
   int row[kTopK];
   float w[kTopK];
 #pragma unroll
@@ -37,10 +39,10 @@ combine_kernel(const uint16_t* __restrict__ down, const int32_t* __restrict__ pa
   uint4 v[kTopK][2];
 #pragma unroll
   for (int k = 0; k < kTopK; ++k) {
-    const uint4* src = (const uint4*)(down + (size_t)max(row[k], 0) * kH + c);
+    const uint16_t* src = down + (size_t)max(row[k], 0) * kH;
     if (row[k] >= 0) {
-      v[k][0] = src[0];
-      v[k][1] = src[1];
+      v[k][0] = *(const uint4*)(src + c0);
+      v[k][1] = *(const uint4*)(src + c1);
     }
   }
   float a[kCombCols];
@@ -68,9 +70,8 @@ combine_kernel(const uint16_t* __restrict__ down, const int32_t* __restrict__ pa
       p[q] = (uint32_t)f32_to_bf16_rne(a[8 * h + 2 * q]) | ((uint32_t)f32_to_bf16_rne(a[8 * h + 2 * q + 1]) << 16);
     o[h] = uint4{p[0], p[1], p[2], p[3]};
   }
-  uint4* dst = (uint4*)(out + (size_t)t * kH + c);
-  dst[0] = o[0];
-  dst[1] = o[1];
+  *(uint4*)(out + (size_t)t * kH + c0) = o[0];
+  *(uint4*)(out + (size_t)t * kH + c1) = o[1];
 }
 
 }  // namespace
