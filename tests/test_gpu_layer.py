@@ -43,6 +43,11 @@ LAYER_CASES = [
     ("small_t64", 240, 37, 37),
     ("small_t64", -16, 21, 21),
     ("prefill_t1024", 256, 128, 8),
+    # token counts on either side of each kernel-choice boundary
+    ("small_t64", None, 17, 17),        # first T past the in-GEMM1 routing
+    ("prefill_t1024", None, 65, 24),    # first T with the tiled GEMM1 and a combine pass
+    ("skewed_t8192", None, 2047, 16),   # largest T of the tiled kernels
+    ("skewed_t8192", None, 2048, 16),   # smallest T of the wide kernels
 ]
 
 
