@@ -92,3 +92,21 @@ def test_route_repeatable(pkg, cuda_device):
     b = pkg.route(tok[0], tok[1], 0, 2.5)
     for x, y in zip(snap, (b.topk_ids, b.topk_w, b.pair_row, b.expert_off, b.perm_token)):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("T", [1, 16, 40])
+def test_exact_ties_go_to_lower_ids(pkg, cuda_device, T):
+    """Exact score ties are exempt from the reference parity above (torch.topk
+    resolves them through nth_element). The GPU resolves them
+    deterministically to the lower group and expert index. With all scores
+    equal, groups 0-3 are kept and experts 0-7 are chosen with equal weights.
+    Covers the single-workgroup (T <= 16) and the multi-workgroup path."""
+    print(f"exact-ties case T={T}", flush=True)
+    logits = torch.zeros((T, 256), dtype=torch.float32, device=cuda_device)
+    bias = torch.zeros(256, dtype=torch.bfloat16, device=cuda_device)
+    r = pkg.route(logits, bias, 0, 2.5)
+    torch.cuda.synchronize()
+    ids = r.topk_ids.cpu()
+    assert (ids == torch.arange(8, dtype=torch.int32)).all()
+    w = r.topk_w.cpu()
+    assert (w == w[0, 0]).all() and abs(float(w[0, 0]) - 2.5 / 8) < 1e-6
