@@ -8,8 +8,10 @@
 // NaN elements do not enter the absmax and encode as NaN.
 //
 // Design (gfx950): HBM-bound (reads 2 B and writes 1 B per element), so the
-// arithmetic per element has to stay under the memory time.  One wave per
-// token row, four rows per workgroup (T/4 workgroups: 256 at T = 1024).  A
+// arithmetic per element has to stay under the memory time.  Up to T = 2048
+// one workgroup per token row, wave p quantising pass p (7 waves per row, so
+// that enough loads are in flight at small T).  Beyond, one wave per token
+// row, four rows per workgroup (T/4 workgroups: 2048 at T = 8192).  A
 // wave issues all 14 row loads (16 B per lane each) before any arithmetic, so
 // a token has its whole 14 KB row in flight at once; each of the 7 passes
 // then covers 1024 columns = 8 scale blocks, 8 lanes per block and 16
@@ -117,6 +119,30 @@ __device__ __forceinline__ uint32_t exact_pack4(float x0, float x1, float x2, fl
          (f32_to_e4m3_satfinite(x2 / s) << 16) | (f32_to_e4m3_satfinite(x3 / s) << 24);
 }
 
+// One pass of a wave: 16 elements per lane (a, b), 8 lanes per scale block;
+// the e4m3 codes and this lane's block scale (wave-uniform fast/exact branch).
+__device__ __forceinline__ void quantize_pass(const uint4& a, const uint4& b, uint4& out, float& s) {
+  const uint32_t m = group8_max_u32(lane_absmax_bits(a, b));
+  const bool odd = m > 0x7F7Fu || (m != 0u && m < kQTinyBf16);
+  const uint32_t e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  if (__ballot(odd) == 0) {
+    const float amax = __uint_as_float(m << 16);
+    s = amax > 0.0f ? amax / 448.0f : 1.0f;
+    const float r = 1.0f / s;
+    out.x = fast_pack4(bf16_lo(e[0]), bf16_hi(e[0]), bf16_lo(e[1]), bf16_hi(e[1]), s, r);
+    out.y = fast_pack4(bf16_lo(e[2]), bf16_hi(e[2]), bf16_lo(e[3]), bf16_hi(e[3]), s, r);
+    out.z = fast_pack4(bf16_lo(e[4]), bf16_hi(e[4]), bf16_lo(e[5]), bf16_hi(e[5]), s, r);
+    out.w = fast_pack4(bf16_lo(e[6]), bf16_hi(e[6]), bf16_lo(e[7]), bf16_hi(e[7]), s, r);
+  } else {
+    const float amax = __uint_as_float(group8_max_u32(lane_absmax_bits_nonnan(a, b)) << 16);
+    s = amax > 0.0f ? amax / 448.0f : 1.0f;
+    out.x = exact_pack4(bf16_lo(e[0]), bf16_hi(e[0]), bf16_lo(e[1]), bf16_hi(e[1]), s);
+    out.y = exact_pack4(bf16_lo(e[2]), bf16_hi(e[2]), bf16_lo(e[3]), bf16_hi(e[3]), s);
+    out.z = exact_pack4(bf16_lo(e[4]), bf16_hi(e[4]), bf16_lo(e[5]), bf16_hi(e[5]), s);
+    out.w = exact_pack4(bf16_lo(e[6]), bf16_hi(e[6]), bf16_lo(e[7]), bf16_hi(e[7]), s);
+  }
+}
+
 __global__ void __launch_bounds__(kQThreads)
 quantize_hidden_kernel(const uint16_t* __restrict__ x, int T, uint8_t* __restrict__ q,
                        float* __restrict__ scale) {
@@ -136,28 +162,9 @@ quantize_hidden_kernel(const uint16_t* __restrict__ x, int T, uint8_t* __restric
     }
 #pragma unroll
     for (int c = 0; c < kQPasses; ++c) {
-      const uint4 a = raw[2 * c], b = raw[2 * c + 1];
-      const uint32_t m = group8_max_u32(lane_absmax_bits(a, b));
-      const bool odd = m > 0x7F7Fu || (m != 0u && m < kQTinyBf16);
-      const uint32_t e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
       uint4 out;
       float s;
-      if (__ballot(odd) == 0) {
-        const float amax = __uint_as_float(m << 16);
-        s = amax > 0.0f ? amax / 448.0f : 1.0f;
-        const float r = 1.0f / s;
-        out.x = fast_pack4(bf16_lo(e[0]), bf16_hi(e[0]), bf16_lo(e[1]), bf16_hi(e[1]), s, r);
-        out.y = fast_pack4(bf16_lo(e[2]), bf16_hi(e[2]), bf16_lo(e[3]), bf16_hi(e[3]), s, r);
-        out.z = fast_pack4(bf16_lo(e[4]), bf16_hi(e[4]), bf16_lo(e[5]), bf16_hi(e[5]), s, r);
-        out.w = fast_pack4(bf16_lo(e[6]), bf16_hi(e[6]), bf16_lo(e[7]), bf16_hi(e[7]), s, r);
-      } else {
-        const float amax = __uint_as_float(group8_max_u32(lane_absmax_bits_nonnan(a, b)) << 16);
-        s = amax > 0.0f ? amax / 448.0f : 1.0f;
-        out.x = exact_pack4(bf16_lo(e[0]), bf16_hi(e[0]), bf16_lo(e[1]), bf16_hi(e[1]), s);
-        out.y = exact_pack4(bf16_lo(e[2]), bf16_hi(e[2]), bf16_lo(e[3]), bf16_hi(e[3]), s);
-        out.z = exact_pack4(bf16_lo(e[4]), bf16_hi(e[4]), bf16_lo(e[5]), bf16_hi(e[5]), s);
-        out.w = exact_pack4(bf16_lo(e[6]), bf16_hi(e[6]), bf16_lo(e[7]), bf16_hi(e[7]), s);
-      }
+      quantize_pass(raw[2 * c], raw[2 * c + 1], out, s);
       *(uint4*)(qrow + c * kQPass) = out;
       if ((lane & (kQLanesPerBlk - 1)) == 0) sc[c * (kQPass / kBlk) + lane / kQLanesPerBlk][w] = s;
     }
@@ -171,9 +178,33 @@ quantize_hidden_kernel(const uint16_t* __restrict__ x, int T, uint8_t* __restric
   }
 }
 
+// Small T (latency-bound with one wave per row): one workgroup per token
+// row, wave p quantises pass p (columns 1024p ..) and writes its 8 block
+// scales directly.  Same arithmetic as above, so the same bits.
+constexpr int kQSmallMaxTokens = 2048;
+
+__global__ void __launch_bounds__(kQPasses * kWave)
+quantize_hidden_rows_kernel(const uint16_t* __restrict__ x, int T, uint8_t* __restrict__ q,
+                            float* __restrict__ scale) {
+  const int t = blockIdx.x;
+  const int c = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint16_t* src = x + (size_t)t * kH + c * kQPass + lane * kQLaneCols;
+  const uint4 a = *(const uint4*)src, b = *(const uint4*)(src + 8);
+  uint4 out;
+  float s;
+  quantize_pass(a, b, out, s);
+  *(uint4*)(q + (size_t)t * kH + c * kQPass + lane * kQLaneCols) = out;
+  if ((lane & (kQLanesPerBlk - 1)) == 0) scale[(size_t)(c * (kQPass / kBlk) + lane / kQLanesPerBlk) * T + t] = s;
+}
+
 }  // namespace
 
 hipError_t launch_quantize_hidden(const uint16_t* x, int T, uint8_t* q, float* scale, hipStream_t stream) {
+  if (T <= kQSmallMaxTokens) {
+    hipLaunchKernelGGL(quantize_hidden_rows_kernel, dim3(T), dim3(kQPasses * kWave), 0, stream, x, T, q, scale);
+    return hipGetLastError();
+  }
   const int blocks = (T + kQTokens - 1) / kQTokens;
   hipLaunchKernelGGL(quantize_hidden_kernel, dim3(blocks), dim3(kQThreads), 0, stream, x, T, q, scale);
   return hipGetLastError();

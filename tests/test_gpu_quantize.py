@@ -22,7 +22,7 @@ def _special_rows():
     return _bf16(x)
 
 
-@pytest.mark.parametrize("T", [1, 15, 16, 17, 300])
+@pytest.mark.parametrize("T", [1, 15, 16, 17, 300, 2048, 2049])  # one row per workgroup up to 2048, four beyond
 def test_quantize_matches_oracle(pkg, orc, cuda_device, T):
     host = _rows(T, seed=T)
     if T >= 3:
