@@ -22,13 +22,28 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t k) {
   return max(max(a, b), max(c, d));
 }
 
-// Maxima of the two half-waves (lanes 0-31, 32-63) of a 32-bit key,
-// wave-uniform.  Four DPP row steps, then rows 1 and 3 take rows 0 and 2.
-__device__ __forceinline__ void halfwave_max(uint32_t k, uint32_t& m0, uint32_t& m1) {
-  k = row16_max_u32(k);
-  k = max(k, dpp_u32<kDppRowBcast15, 0xA>(k));
-  m0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 31);
-  m1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 63);
+// The two largest 32-bit keys (a repeated maximum counts twice) of each
+// half-wave (lanes 0-31, 32-63), wave-uniform, in one reduction: every step
+// merges a lane's pair (a >= b) with a partner's.  Four DPP row steps, then
+// rows 1 and 3 merge rows 0 and 2 (row_bcast:15; rows 0 and 2 merge with
+// the pair (0, 0), key 0 lying below every real score).
+__device__ __forceinline__ void merge_top2(uint32_t& a, uint32_t& b, uint32_t pa, uint32_t pb) {
+  const uint32_t lo = min(a, pa);
+  a = max(a, pa);
+  b = max(max(b, pb), lo);
+}
+__device__ __forceinline__ void halfwave_top2(uint32_t k, uint32_t& a0, uint32_t& b0, uint32_t& a1, uint32_t& b1) {
+  uint32_t a = k, b = 0u;
+  merge_top2(a, b, dpp_u32<kDppQuad1032, 0xF>(a), dpp_u32<kDppQuad1032, 0xF>(b));
+  merge_top2(a, b, dpp_u32<kDppQuad2301, 0xF>(a), dpp_u32<kDppQuad2301, 0xF>(b));
+  merge_top2(a, b, dpp_u32<kDppRowHalfMirror, 0xF>(a), dpp_u32<kDppRowHalfMirror, 0xF>(b));
+  merge_top2(a, b, dpp_u32<kDppRowMirror, 0xF>(a), dpp_u32<kDppRowMirror, 0xF>(b));
+  merge_top2(a, b, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a, kDppRowBcast15, 0xA, 0xF, false),
+             (uint32_t)__builtin_amdgcn_update_dpp(0, (int)b, kDppRowBcast15, 0xA, 0xF, false));
+  a0 = (uint32_t)__builtin_amdgcn_readlane((int)a, 31);
+  b0 = (uint32_t)__builtin_amdgcn_readlane((int)b, 31);
+  a1 = (uint32_t)__builtin_amdgcn_readlane((int)a, 63);
+  b1 = (uint32_t)__builtin_amdgcn_readlane((int)b, 63);
 }
 
 // Routes token t with one wavefront.  Returns the 8 selected ids, ascending
@@ -57,19 +72,12 @@ __device__ inline void route_token(const float* __restrict__ logits, const uint1
   // moe.py:135-136: group score = sum of the two largest biased scores (a
   // repeated maximum counts twice).  The four slots reduce independently.
   float G[kNGroup];
-  uint32_t m1[4][2], m2[4][2];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) halfwave_max(key[j], m1[j][0], m1[j][1]);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t mine = lane < 32 ? m1[j][0] : m1[j][1];
-    const uint64_t eq = __ballot(key[j] == mine);
-    // drop one instance of the maximum (the lowest lane holding it)
-    const int lo0 = __builtin_ctzll(eq & 0x00000000FFFFFFFFull);
-    const int lo1 = __builtin_ctzll(eq & 0xFFFFFFFF00000000ull);
-    halfwave_max(lane == lo0 || lane == lo1 ? 0u : key[j], m2[j][0], m2[j][1]);
-    G[2 * j] = float_from_order_key(m1[j][0]) + float_from_order_key(m2[j][0]);
-    G[2 * j + 1] = float_from_order_key(m1[j][1]) + float_from_order_key(m2[j][1]);
+    uint32_t a0, b0, a1, b1;
+    halfwave_top2(key[j], a0, b0, a1, b1);
+    G[2 * j] = float_from_order_key(a0) + float_from_order_key(b0);
+    G[2 * j + 1] = float_from_order_key(a1) + float_from_order_key(b1);
   }
   // moe.py:139-146: keep the top-4 groups (ties -> lower group index).
   uint32_t keep = 0;
