@@ -11,7 +11,7 @@
 //     owns experts l, l+64, l+128, l+192, so a routing group of 32 experts is
 //     one half-wave in one register slot;
 //   * scores become 32-bit order-preserving keys; the group top-2 sums use
-//     DPP max-reductions per half-wave (four slots in parallel), and the
+//     one DPP top-2 reduction per half-wave (four slots in parallel), and the
 //     top-8 is eight rounds of a DPP wave maximum plus ballots for the lowest
 //     expert holding it, the ids then sorted by a comparator network;
 //   * T <= 16 (decode): the single workgroup also builds the permutation from
