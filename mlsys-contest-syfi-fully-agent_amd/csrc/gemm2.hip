@@ -229,8 +229,11 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
 //     with scale 1); P accumulates the two stages of a 128-K scale block on
 //     v_mfma_f32_16x16x32_bf16, then acc += P * w_scale[n/128, kb].
 // ---------------------------------------------------------------------------
-// Token count from which GEMM2 uses the wide 256 x 256 tiles (below: 64 x 128
-// tiles of 8 waves, measured fastest at T = 1024).
+// Token count from which GEMM2 uses the wide 256 x 256 tiles.  Below it,
+// 64 x 256 tiles of 8 waves with a 3-stage ring: at T = 1024 they ran 95 us
+// against 104 us for 64 x 128 tiles with 4 stages.  The wider tile copies each
+// activation row once per 256 weight rows instead of once per 128, and at
+// 72 KB of LDS two workgroups still fit on a CU.
 constexpr int kGemm2TiledLargeMinTokens = 2048;
 
 template <int WM, int WN, int MI, int NJ>
@@ -247,7 +250,7 @@ struct G2Tiled {
   static constexpr int kBOff = kAFrags * 2048;
   static constexpr int kStageBytes = kBOff + kBFrags * 1024;
   static constexpr int kWscBytes = WN * kNIBlk * 4;  // weight block scales (after the stages)
-  static constexpr int kStages = 4;
+  static constexpr int kStages = 3;
   static_assert(kStages >= 2 && kStages <= 5, "pipeline depth");
   static constexpr int kSteps = kI / 64;  // stages per tile (two per scale block)
   static constexpr int kPlanes = 2 * kAFrags + kBFrags;
@@ -620,7 +623,7 @@ hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const L
                        (const int32_t*)(ws + L.perm_token), (const float*)(ws + L.perm_w), T, (uint16_t*)out);
     return hipGetLastError();
   }
-  if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<2, 4, 2, 2>(T, w2, w2_scale, L, ws, stream);
+  if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<2, 4, 2, 4>(T, w2, w2_scale, L, ws, stream);
   return launch_gemm2_wide(T, w2, w2_scale, L, ws, stream);
 }
 
