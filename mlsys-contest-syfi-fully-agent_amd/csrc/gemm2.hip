@@ -233,8 +233,11 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
 // 64 x 256 tiles of 8 waves with a 3-stage ring: at T = 1024 they ran 95 us
 // against 104 us for 64 x 128 tiles with 4 stages.  The wider tile copies each
 // activation row once per 256 weight rows instead of once per 128, and at
-// 72 KB of LDS two workgroups still fit on a CU.
-constexpr int kGemm2TiledLargeMinTokens = 2048;
+// 72 KB of LDS two workgroups still fit on a CU.  They also beat the wide
+// tiles up to T = 4096 (T = 2048: 138 against 195-211 us); where they lose
+// depends on the rows per active expert, which the host does not know: with
+// four hot experts they tie at T = 4096 and trail by 2.5% at T = 6144.
+constexpr int kGemm2TiledLargeMinTokens = 4096;
 
 template <int WM, int WN, int MI, int NJ>
 struct G2Tiled {
