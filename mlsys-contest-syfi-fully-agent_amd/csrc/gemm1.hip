@@ -338,8 +338,12 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
 // ---------------------------------------------------------------------------
 // Token count from which GEMM1 uses the wide 256 x 256 tiles.  Below it,
 // experts have few rows, and 64-row x 64-gate-column tiles of 8 waves give
-// more workgroups to stream the weights (measured fastest at T = 1024).
-constexpr int kGemm1TiledLargeMinTokens = 2048;
+// more workgroups to stream the weights.  Measured: at T = 1536 the wide
+// tiles win with uniform routing (222 against 234 us) and with four hot
+// experts (319 against 430 us); at T = 1024 the tiled kernel wins with uniform
+// routing (188 against 206 us) and loses with hot experts (320 against 222 us).
+// Both kernels give the same output bits.
+constexpr int kGemm1TiledLargeMinTokens = 1025;
 
 template <int WM, int WN, int MI>
 struct G1Tiled {

@@ -46,8 +46,10 @@ LAYER_CASES = [
     # token counts on either side of each kernel-choice boundary
     ("small_t64", None, 17, 17),        # first T past the in-GEMM1 routing
     ("prefill_t1024", None, 65, 24),    # first T with the tiled GEMM1 and a combine pass
-    ("skewed_t8192", None, 2047, 16),   # largest T of the tiled kernels
-    ("skewed_t8192", None, 2048, 16),   # smallest T of the wide GEMM1
+    ("skewed_t8192", None, 1024, 16),   # largest T of the tiled GEMM1
+    ("skewed_t8192", None, 1025, 16),   # smallest T of the wide GEMM1
+    ("skewed_t8192", None, 2047, 16),
+    ("skewed_t8192", None, 2048, 16),
     ("skewed_t8192", None, 4095, 16),   # largest T of the tiled GEMM2
     ("skewed_t8192", None, 4096, 16),   # smallest T of the wide GEMM2
 ]
