@@ -114,7 +114,8 @@ typedef struct {
   size_t perm_token; /* int32 [8T]     token of each permuted row                 */
   size_t perm_w;     /* float [8T]     combination weight of each permuted row    */
   size_t act;        /* bf16  [8T, 2048] SwiGLU output rows                       */
-  size_t down;       /* bf16  [8T, 7168] GEMM2 output rows                        */
+  size_t down;       /* bf16  [8T, 7168] GEMM2 output rows (T > 64 only; for
+                        T <= 64 GEMM2 combines in registers and the region is empty) */
   size_t block_hist; /* int32 [workgroups, 32] local-expert pairs per routing workgroup
                         (T > 16; ceil(T/4) workgroups up to T = 1024, ceil(T/16) beyond) */
   size_t total;      /* = moe_fp8_ds_workspace_size(T)                            */
@@ -128,7 +129,7 @@ int moe_fp8_ds_workspace_layout(int64_t T, moe_fp8_ds_layout* layout);
  * [T,7168] per 128-column block: scale = absmax/448 (1 for an all-zero
  * block; NaN does not enter the absmax), q = e4m3(x/scale) rounded to nearest
  * even and saturated to +-448; scales are written transposed, [56,T].
- * hidden_bf16 must be 16-byte aligned, hidden_fp8 8-byte aligned.  Stream
+ * hidden_bf16 and hidden_fp8 must be 16-byte aligned, hidden_scale 4-byte.  Stream
  * ordered, no allocation, T == 0 is a no-op. */
 int moe_fp8_ds_quantize_hidden(const void* hidden_bf16, int64_t T, void* hidden_fp8, float* hidden_scale,
                                hipStream_t stream);

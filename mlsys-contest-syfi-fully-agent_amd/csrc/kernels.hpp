@@ -14,8 +14,8 @@ bool gemm1_routes(int T);
 hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
                         const float* w13_scale, const float* logits, const uint16_t* bias, float rsf,
                         int64_t offset, const Layout& L, char* ws, hipStream_t stream);
-// Largest T for which GEMM2 also performs the weighted combine (no combine pass).
-constexpr int kGemm2StreamMaxTokens = 64;
+// T <= kGemm2StreamMaxTokens (moe_common.hpp): GEMM2 also performs the
+// weighted combine, and no combine pass runs.
 bool gemm2_fuses_combine(int T);
 hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws, void* out,
                         hipStream_t stream);

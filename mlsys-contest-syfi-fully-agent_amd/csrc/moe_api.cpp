@@ -154,7 +154,8 @@ int moe_fp8_ds_quantize_hidden(const void* hidden_bf16, int64_t T, void* hidden_
   if (T < 0 || T > moe::kMaxTokens) return MOE_FP8_DS_ERR_SHAPE;
   if (T == 0) return MOE_FP8_DS_OK;
   if (!hidden_bf16 || !hidden_fp8 || !hidden_scale) return MOE_FP8_DS_ERR_NULL;
-  if (!aligned16(hidden_bf16) || ((uintptr_t)hidden_fp8 & 7u) || ((uintptr_t)hidden_scale & 3u))
+  // the kernel stores e4m3 rows 16 bytes at a time
+  if (!aligned16(hidden_bf16) || !aligned16(hidden_fp8) || ((uintptr_t)hidden_scale & 3u))
     return MOE_FP8_DS_ERR_ALIGN;
   const hipError_t err = moe::launch_quantize_hidden((const uint16_t*)hidden_bf16, (int)T, (uint8_t*)hidden_fp8,
                                                      hidden_scale, stream);

@@ -24,21 +24,29 @@ constexpr int kNIBlk = kI / kBlk;   // 16
 constexpr int kN2IBlk = k2I / kBlk; // 32
 constexpr int kWave = 64;
 
-// Largest T any entry point accepts: keeps every row index (< 8T) and every
-// grid dimension inside int32 / HIP limits.
-constexpr int64_t kMaxTokens = 1 << 20;
+// Largest T any entry point accepts.  Every row index (< 8T) and grid
+// dimension stays inside int32, and every byte offset of a token row inside
+// hidden_states (token * 7168 + 7167) inside uint32: the wide GEMM1 builds
+// its copy addresses as a wave-uniform base plus a 32-bit lane offset, which
+// would wrap from token 599,187 (2^32 / 7168) on.
+constexpr int64_t kMaxTokens = 1 << 19;
+static_assert(kMaxTokens * kH <= (int64_t)1 << 32, "token row offsets fit in 32 bits");
+
+// Largest T for which GEMM2 also performs the weighted combine: its rows
+// never reach the workspace, and no combine pass runs.
+constexpr int kGemm2StreamMaxTokens = 64;
 
 struct Layout {
   size_t topk_ids, topk_w, pair_row, expert_off, perm_token, perm_w, act, down, block_hist, total;
 };
 
-inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+constexpr size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-inline Layout make_layout(int64_t T) {
+constexpr Layout make_layout(int64_t T) {
   Layout L{};
   size_t off = 0;
-  auto take = [&](size_t bytes) {
-    size_t at = off;
+  auto take = [&off](size_t bytes) {
+    const size_t at = off;
     off = align_up(off + bytes, 256);
     return at;
   };
@@ -50,7 +58,8 @@ inline Layout make_layout(int64_t T) {
   L.perm_token = take(rows * sizeof(int32_t));
   L.perm_w = take(rows * sizeof(float));
   L.act = take(rows * kI * sizeof(uint16_t));
-  L.down = take(rows * kH * sizeof(uint16_t));
+  // GEMM2 rows exist only where a separate combine pass reads them
+  L.down = take(T > kGemm2StreamMaxTokens ? rows * kH * sizeof(uint16_t) : 0);
   L.block_hist = take((size_t)((T + 3) / 4) * kELocal * sizeof(int32_t));  // per route workgroup (4 tokens)
   L.total = off;
   return L;

@@ -27,8 +27,8 @@ from . import _lib
 
 H, I, E_LOCAL, E_GLOBAL, TOP_K, BLOCK = 7168, 2048, 32, 256, 8, 128
 # Up to this T the GEMM2 kernel also performs the weighted combine and the
-# workspace's GEMM2 rows (`down`) are not written (kGemm2StreamMaxTokens in
-# csrc/kernels.hpp).
+# workspace holds no GEMM2 rows (`down`; kGemm2StreamMaxTokens in
+# csrc/moe_common.hpp).
 FUSED_COMBINE_MAX_TOKENS = 64
 
 _ws_lock = threading.Lock()
@@ -151,7 +151,9 @@ class RouteResult:
         self.perm_token = view(lay.perm_token, T * TOP_K, torch.int32)
         self.perm_w = view(lay.perm_w, T * TOP_K, torch.float32)
         self.act = view(lay.act, T * TOP_K * I, torch.int16).view(T * TOP_K, I)
-        self.down = view(lay.down, T * TOP_K * H, torch.int16).view(T * TOP_K, H)
+        # GEMM2 rows reach the workspace only where a combine pass reads them
+        self.down = (view(lay.down, T * TOP_K * H, torch.int16).view(T * TOP_K, H)
+                     if T > FUSED_COMBINE_MAX_TOKENS else None)
         # one row per routing workgroup: 4 tokens each up to T = 1024, 16 beyond
         blocks = (T + 3) // 4 if T <= 1024 else (T + 15) // 16
         self.block_hist = view(lay.block_hist, blocks * E_LOCAL, torch.int32).view(-1, E_LOCAL)
