@@ -49,7 +49,8 @@ typedef enum {
   MOE_FP8_DS_ERR_ALIGN = -3,     /* a pointer is not 16-byte aligned           */
   MOE_FP8_DS_ERR_WORKSPACE = -4, /* workspace smaller than workspace_size(T)   */
   MOE_FP8_DS_ERR_HIP = -5,       /* a HIP launch failed                        */
-  MOE_FP8_DS_ERR_ARG = -6        /* non-finite routed_scaling_factor           */
+  MOE_FP8_DS_ERR_ARG = -6,       /* non-finite routed_scaling_factor           */
+  MOE_FP8_DS_ERR_SCRATCH = -7    /* T > MOE_FP8_DS_NOALLOC_MAX_TOKENS (moe_fp8_ds_run_noalloc) */
 } moe_fp8_ds_status;
 
 /* Library version (MOE_FP8_DS_VERSION of the build). */
@@ -78,6 +79,31 @@ int moe_fp8_ds_run(const float* routing_logits, const void* routing_bias,
                    const void* gemm2_weights, const float* gemm2_weights_scale,
                    int64_t local_expert_offset, double routed_scaling_factor, void* output,
                    int64_t T, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Largest T moe_fp8_ds_run_noalloc accepts. */
+#define MOE_FP8_DS_NOALLOC_MAX_TOKENS 64
+
+/* moe_fp8_ds_run without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference, whose
+ * run_impl grows a hidden global workspace with cudaMalloc
+ * (moe/solution/cuda/moe.cu:2511-2589).
+ *
+ * The intermediates live in a static device array inside the library, sized
+ * for MOE_FP8_DS_NOALLOC_MAX_TOKENS tokens (decode and small batches; the
+ * workspace size for 64 tokens, about 2 MB, held on every device the library runs on until the process ends).
+ * T above that returns MOE_FP8_DS_ERR_SCRATCH.  The call allocates nothing
+ * and, like moe_fp8_ds_run, needs no initialised scratch.  It uses the
+ * scratch of the current device (the stream must belong to it), and every
+ * call on one device shares that scratch: calls that overlap on one device
+ * (concurrent streams or host threads) race and must be serialised by the
+ * caller.  Results are bit-identical to moe_fp8_ds_run's. */
+int moe_fp8_ds_run_noalloc(const float* routing_logits, const void* routing_bias,
+                           const void* hidden_states, const float* hidden_states_scale,
+                           const void* gemm1_weights, const float* gemm1_weights_scale,
+                           const void* gemm2_weights, const float* gemm2_weights_scale,
+                           int64_t local_expert_offset, double routed_scaling_factor, void* output,
+                           int64_t T, hipStream_t stream);
 
 /* Number of device stages of moe_fp8_ds_run: routing + permutation, GEMM1 +
  * SwiGLU, GEMM2, combine.  For T <= 16 the routing runs inside GEMM1 (stage 0

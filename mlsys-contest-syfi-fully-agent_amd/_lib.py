@@ -13,7 +13,9 @@ MOE_LIB = os.path.join(LIB_DIR, "libmoe_fp8_ds.so")
 SYNTH_LIB = os.path.join(LIB_DIR, "libmoe_synth.so")
 
 # moe_fp8_ds_status (include/moe_fp8_ds.h)
-OK, ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP, ERR_ARG = 0, -1, -2, -3, -4, -5, -6
+OK, ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP, ERR_ARG, ERR_SCRATCH = 0, -1, -2, -3, -4, -5, -6, -7
+# MOE_FP8_DS_NOALLOC_MAX_TOKENS: largest T of moe_fp8_ds_run_noalloc
+NOALLOC_MAX_TOKENS = 64
 
 
 class Layout(ctypes.Structure):
@@ -49,6 +51,8 @@ def moe_lib() -> ctypes.CDLL:
         L.moe_fp8_ds_run.restype = ctypes.c_int
         L.moe_fp8_ds_run_profiled.argtypes = [P, P, P, P, P, P, P, P, i64, dbl, P, i64, P, sz, P, P]
         L.moe_fp8_ds_run_profiled.restype = ctypes.c_int
+        L.moe_fp8_ds_run_noalloc.argtypes = [P, P, P, P, P, P, P, P, i64, dbl, P, i64, P]
+        L.moe_fp8_ds_run_noalloc.restype = ctypes.c_int
         L.moe_fp8_ds_route.argtypes = [P, P, i64, dbl, i64, P, sz, P]
         L.moe_fp8_ds_route.restype = ctypes.c_int
         L.moe_fp8_ds_quantize_hidden.argtypes = [P, i64, P, P, P]

@@ -6,11 +6,41 @@
 // (the caller's stream), no host synchronisation at any T (the device builds
 // the expert schedule), and status codes instead of unchecked CUDA calls.
 #include <cmath>
+#include <mutex>
 
 #include "../../include/moe_fp8_ds.h"
 #include "kernels.hpp"
 
 namespace {
+
+// ---- scratch of the no-allocation entry point -----------------------------
+// moe_fp8_ds_run_noalloc keeps its intermediates in this file-scope device
+// array instead of a caller workspace: the layer's workspace layout for
+// MOE_FP8_DS_NOALLOC_MAX_TOKENS tokens.  Each device the library runs on
+// holds its own copy (loaded with the code object) until the process ends.
+// In host code `scratch` only names the symbol; its device address comes from
+// hipGetSymbolAddress, once per device (noalloc_scratch).
+constexpr size_t kNoAllocScratchBytes = moe::make_layout(MOE_FP8_DS_NOALLOC_MAX_TOKENS).total;
+static_assert(kNoAllocScratchBytes <= (size_t)8 << 20, "the no-allocation scratch stays small");
+__device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch, looked up on the first call
+// on that device; nullptr on failure.
+void* noalloc_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -39,6 +69,7 @@ const char* moe_fp8_ds_status_string(int status) {
     case MOE_FP8_DS_ERR_WORKSPACE: return "workspace too small";
     case MOE_FP8_DS_ERR_HIP: return "HIP launch failed";
     case MOE_FP8_DS_ERR_ARG: return "invalid scalar argument";
+    case MOE_FP8_DS_ERR_SCRATCH: return "T exceeds MOE_FP8_DS_NOALLOC_MAX_TOKENS (no-allocation entry point)";
     default: return "unknown status";
   }
 }
@@ -147,6 +178,23 @@ int moe_fp8_ds_run_profiled(const float* routing_logits, const void* routing_bia
                    gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
                    routed_scaling_factor, output, T, workspace, workspace_bytes, stream,
                    stage_events);
+}
+
+int moe_fp8_ds_run_noalloc(const float* routing_logits, const void* routing_bias, const void* hidden_states,
+                           const float* hidden_states_scale, const void* gemm1_weights,
+                           const float* gemm1_weights_scale, const void* gemm2_weights,
+                           const float* gemm2_weights_scale, int64_t local_expert_offset,
+                           double routed_scaling_factor, void* output, int64_t T, hipStream_t stream) {
+  if (T < 0) return MOE_FP8_DS_ERR_SHAPE;
+  if (T > MOE_FP8_DS_NOALLOC_MAX_TOKENS) return MOE_FP8_DS_ERR_SCRATCH;
+  if (T == 0) return MOE_FP8_DS_OK;
+  void* ws = noalloc_scratch();
+  if (!ws) return MOE_FP8_DS_ERR_HIP;
+  // The layer needs no initialised workspace (every region it reads is
+  // written earlier in the same call), so nothing is cleared here.
+  return run_layer(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                   gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+                   routed_scaling_factor, output, T, ws, kNoAllocScratchBytes, stream, nullptr);
 }
 
 int moe_fp8_ds_quantize_hidden(const void* hidden_bf16, int64_t T, void* hidden_fp8, float* hidden_scale,

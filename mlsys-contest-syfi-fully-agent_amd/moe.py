@@ -106,6 +106,26 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_
     return output
 
 
+def run_noalloc(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+                gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
+                routed_scaling_factor, output):
+    """`run` through moe_fp8_ds_run_noalloc: no workspace, nothing allocated
+    (usable under stream capture).  T <= NOALLOC_MAX_TOKENS (64); the
+    library's one static scratch per device is shared by every such call, so
+    overlapping calls on one device race."""
+    T = _check(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
+               gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, output)
+    dev = routing_logits.device
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    rc = _lib.moe_lib().moe_fp8_ds_run_noalloc(
+        _ptr(routing_logits), _ptr(routing_bias), _ptr(hidden_states), _ptr(hidden_states_scale),
+        _ptr(gemm1_weights), _ptr(gemm1_weights_scale), _ptr(gemm2_weights), _ptr(gemm2_weights_scale),
+        int(local_expert_offset), float(routed_scaling_factor), _ptr(output), T, stream)
+    if rc != _lib.OK:
+        raise RuntimeError(f"moe_fp8_ds_run_noalloc: {_lib.status_string(rc)} ({rc})")
+    return output
+
+
 def quantize_hidden(hidden_states, hidden_states_fp8=None, hidden_states_scale=None):
     """The step before the layer: bf16 hidden rows [T, 7168] -> the layer's
     `hidden_states` (e4m3, [T, 7168]) and `hidden_states_scale` (fp32, [56, T],

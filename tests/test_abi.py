@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol(pkg, header, lib):
 def test_version_and_status_strings(pkg):
     L = pkg._lib.moe_lib()
     assert L.moe_fp8_ds_version() == 1
-    for rc in (0, -1, -2, -3, -4, -5, -6):
+    for rc in (0, -1, -2, -3, -4, -5, -6, -7):
         assert pkg._lib.status_string(rc) != "unknown status"
     assert pkg._lib.status_string(-99) == "unknown status"
 
@@ -61,6 +61,22 @@ def test_max_tokens_keeps_row_offsets_in_32_bits(pkg):
     assert (tmax - 1) * 7168 + 7167 < 2 ** 32
     assert tmax >= 14107  # the contest dataset's largest T (moe.py:13)
     assert L.moe_fp8_ds_workspace_size(tmax) > 0
+
+
+def test_noalloc_validation_without_gpu(pkg):
+    """moe_fp8_ds_run_noalloc refuses T beyond its scratch before any HIP call."""
+    L = pkg._lib.moe_lib()
+    buf = ctypes.create_string_buffer(64 + 256)
+    base = ctypes.addressof(buf)
+    al = base + (-base) % 256  # never dereferenced
+    p = al
+    lim = pkg._lib.NOALLOC_MAX_TOKENS
+    assert L.moe_fp8_ds_run_noalloc(p, p, p, p, p, p, p, p, 0, 2.5, p, lim + 1, None) == pkg._lib.ERR_SCRATCH
+    assert L.moe_fp8_ds_run_noalloc(p, p, p, p, p, p, p, p, 0, 2.5, p, -1, None) == -2
+    assert L.moe_fp8_ds_run_noalloc(p, p, p, p, p, p, p, p, 0, 2.5, p, 0, None) == 0
+    # the header's limit is what the library enforces
+    hdr = open(os.path.join(ROOT, "include", "moe_fp8_ds.h")).read()
+    assert re.search(r"#define MOE_FP8_DS_NOALLOC_MAX_TOKENS (\d+)", hdr).group(1) == str(lim)
 
 
 def _run(L, ptr, T, ws, ws_bytes, rsf=2.5, out=None):
