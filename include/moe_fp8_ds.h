@@ -91,7 +91,7 @@ int moe_fp8_ds_run(const float* routing_logits, const void* routing_bias,
  *
  * The intermediates live in a static device array inside the library, sized
  * for MOE_FP8_DS_NOALLOC_MAX_TOKENS tokens (decode and small batches; the
- * workspace size for 64 tokens, about 2 MB, held on every device the library runs on until the process ends).
+ * workspace size for 64 tokens, about 4.2 MB, held on every device the library runs on until the process ends).
  * T above that returns MOE_FP8_DS_ERR_SCRATCH.  The call allocates nothing
  * and, like moe_fp8_ds_run, needs no initialised scratch.  It uses the
  * scratch of the current device (the stream must belong to it), and every
@@ -139,8 +139,9 @@ typedef struct {
   size_t expert_off; /* int32 [33]     row offsets per local expert; [32] = N_sel */
   size_t perm_token; /* int32 [8T]     token of each permuted row                 */
   size_t perm_w;     /* float [8T]     combination weight of each permuted row    */
-  size_t act;        /* bf16  [8T, 2048] SwiGLU output rows                       */
-  size_t down;       /* bf16  [8T, 7168] GEMM2 output rows (T > 64 only; for
+  size_t act;        /* bf16 pairs [8T, 4096]: SwiGLU output rows, value = hi + lo;
+                        per 64-column chunk c, 64 hi then 64 lo bf16 (8 KB/row)   */
+  size_t down;       /* float [8T, 7168] GEMM2 output rows (T > 64 only; for
                         T <= 64 GEMM2 combines in registers and the region is empty) */
   size_t block_hist; /* int32 [workgroups, 32] local-expert pairs per routing workgroup
                         (T > 16; ceil(T/4) workgroups up to T = 1024, ceil(T/16) beyond) */

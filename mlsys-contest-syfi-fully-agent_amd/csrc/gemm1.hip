@@ -63,8 +63,8 @@ struct S1TileOps {
 // until the next item's loads are out (a store issued before them would
 // delay the wait for them).
 struct S1Out {
-  uint16_t v;
-  int row;  // destination act row, -1: none
+  uint16_t hi, lo;  // the activation as a bf16 pair (split_bf16)
+  int row;          // destination act row, -1: none
 };
 
 // kDirect: the workgroup routes the T tokens itself (route_small, from the
@@ -129,13 +129,6 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     lds_barrier();
   }
 
-  // W13 row of this lane for an item: gate rows 8cg.. in lanes r < 8, the
-  // matching up rows 2048 + 8cg.. in lanes r >= 8.
-  auto w_row = [&](int item) {
-    const int cg = item % kS1Groups;
-    const int e = nth_set_bit(active, item / kS1Groups);
-    return (size_t)e * k2I + (lr < 8 ? 8 * cg + lr : kI + 8 * cg + (lr - 8));
-  };
   // An item's weights of this wave -> its LDS buffer, as 14 wide planes
   // (K block j, rows 8h .. 8h+7 of the item's 16: gate rows 8cg.., then up
   // rows 2048 + 8cg..), 128 bytes per row, chunks swizzled: each copy
@@ -192,7 +185,6 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
   // Multiply a landed tile, reduce the 8 K-partials in a fixed order, SwiGLU,
   // store the activation rows.
   auto compute_tile = [&](int item, int rt, const S1TileOps& o, const v8i (&b)[kS1KB], S1Out& out) {
-    const int cg = item % kS1Groups;
     const int e = nth_set_bit(active, item / kS1Groups);
     const int row0 = X.begin(e);
     const int M = X.end(e) - row0;
@@ -226,13 +218,17 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
       const int r = 4 * lq + i;
       const int prow = kDirect ? (r < rows ? inv[r] : -1) : (r < rows ? row0 + rt * 16 + r : -1);
       const float silu = x2 / (1.0f + expf(-x2));
-      out.v = f32_to_bf16_rne(silu * v);
+      split_bf16(silu * v, out.hi, out.lo);
       out.row = lr < 8 ? prow : -1;
     }
     lds_barrier();  // red / sa / inv consumed before they are rewritten
   };
   auto store_out = [&](int item, const S1Out& out) {
-    if (wave < 4 && out.row >= 0) act[(size_t)out.row * kI + 8 * (item % kS1Groups) + lr] = out.v;
+    if (wave < 4 && out.row >= 0) {
+      uint16_t* p = act + (size_t)out.row * kActRowElems + act_col(8 * (item % kS1Groups) + lr);
+      p[0] = out.hi;
+      p[64] = out.lo;
+    }
   };
 
   // Persistent: the grid is at most what fits on the device at once, and
@@ -564,7 +560,11 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
         if (r < rows) {
           const float x1 = acc[mi][nj][i], x2 = acc[mi][nj + 2][i];
           const float silu = x2 / (1.0f + expf(-x2));
-          act[(size_t)(row0 + r) * kI + j0 + 32 * wn + 16 * nj + lr] = f32_to_bf16_rne(silu * x1);
+          uint16_t hi, lo;
+          split_bf16(silu * x1, hi, lo);
+          uint16_t* p = act + (size_t)(row0 + r) * kActRowElems + act_col(j0 + 32 * wn + 16 * nj + lr);
+          p[0] = hi;
+          p[64] = lo;
         }
       }
   }
@@ -803,17 +803,23 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
   for (int mi = 0; mi < C::MI; ++mi) {
     const int r = C::MI * 16 * wm + 16 * mi + lr;
     if (r < rows) {
-      uint16_t* arow = act + (size_t)(row0 + r) * kI + j0 + 16 * C::NJ * wn + 4 * lq;
+      uint16_t* arow = act + (size_t)(row0 + r) * kActRowElems;
+      const int c0 = j0 + 16 * C::NJ * wn + 4 * lq;  // 4 adjacent columns: one 8-byte store per half
 #pragma unroll
       for (int nj = 0; nj < C::NJ; ++nj) {
-        uint32_t h[4];
+        uint32_t h[4], l[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float x1 = acc[mi][nj][i], x2 = acc[mi][C::NJ + nj][i];
           const float silu = x2 / (1.0f + expf(-x2));
-          h[i] = f32_to_bf16_rne(silu * x1);
+          uint16_t hi, lo;
+          split_bf16(silu * x1, hi, lo);
+          h[i] = hi;
+          l[i] = lo;
         }
-        *(uint2*)(arow + 16 * nj) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        uint16_t* p = arow + act_col(c0 + 16 * nj);
+        *(uint2*)p = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        *(uint2*)(p + 64) = uint2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
       }
     }
   }

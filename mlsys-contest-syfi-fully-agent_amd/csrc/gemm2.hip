@@ -58,7 +58,8 @@ __device__ __forceinline__ S2Job s2_next(const ExpertRows& X, uint32_t active, S
 }
 
 struct S2Regs {
-  v4i a[kS2KB][2][2];  // bf16 act: elements 64g + 16q + 8h .. +7
+  v4i a[kS2KB][2][2];  // act hi: columns 64g + 16q + 8h .. +7 of each of this wave's scale blocks
+  v4i al[kS2KB][2][2]; // act lo, same columns
   float sw[kS2KB];
   int tok;           // token and weight of the row this thread combines
   float pw;          //   (row = (tid / 16) % 16 of the tile)
@@ -74,13 +75,18 @@ __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
   const int crow = row0 + min((int)(threadIdx.x >> 4) & 15, rows - 1);
   R.tok = perm_token[crow];
   R.pw = perm_w[crow];
-  const uint16_t* ap = act + (size_t)(row0 + min(lr, rows - 1)) * kI + kb0 * kBlk + 16 * lq;
+  const uint16_t* ap = act + (size_t)(row0 + min(lr, rows - 1)) * kActRowElems + 16 * lq;
 #pragma unroll
   for (int k = 0; k < kS2KB; ++k) {
 #pragma unroll
     for (int g = 0; g < 2; ++g)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) R.a[k][g][h] = *(const v4i*)(ap + k * kBlk + 64 * g + 8 * h);
+      for (int h = 0; h < 2; ++h) {
+        // column (kb0 + k) * 128 + 64 g + 16 q + 8 h: 64-column chunk 2 (kb0 + k) + g
+        const uint16_t* c = ap + (2 * (kb0 + k) + g) * 128 + 8 * h;
+        R.a[k][g][h] = *(const v4i*)c;
+        R.al[k][g][h] = *(const v4i*)(c + 64);
+      }
     R.sw[k] = w2_scale[((size_t)j.e * kNHBlk + n0 / kBlk) * kNIBlk + kb0 + k];
   }
 }
@@ -173,10 +179,12 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
         v4f p = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][0]),
-                                 e4m3x8_to_bf16((uint32_t)b[nb][k][g][0], (uint32_t)b[nb][k][g][1]), p);
-          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][1]),
-                                 e4m3x8_to_bf16((uint32_t)b[nb][k][g][2], (uint32_t)b[nb][k][g][3]), p);
+          const v8bf b0 = e4m3x8_to_bf16((uint32_t)b[nb][k][g][0], (uint32_t)b[nb][k][g][1]);
+          const v8bf b1 = e4m3x8_to_bf16((uint32_t)b[nb][k][g][2], (uint32_t)b[nb][k][g][3]);
+          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][0]), b0, p);
+          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][1]), b1, p);
+          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.al[k][g][0]), b0, p);
+          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.al[k][g][1]), b1, p);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], cur.sw[k], acc[i]);
@@ -239,7 +247,7 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
 // four hot experts they tie at T = 4096 and trail by 2.5% at T = 6144.
 constexpr int kGemm2TiledLargeMinTokens = 4096;
 
-template <int WM, int WN, int MI, int NJ>
+template <int WM, int WN, int MI, int NJ, int STAGES>
 struct G2Tiled {
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = kWave * kWaves;
@@ -249,25 +257,27 @@ struct G2Tiled {
   static constexpr int kNT = kH / BN;
   static_assert(kH % BN == 0, "column tiles");
   static constexpr int kAFrags = BM / 16;
+  static constexpr int kAFragBytes = 4096;  // hi (two wide planes), then lo (two wide planes)
+  static constexpr int kAPlanes = 4 * kAFrags;
   static constexpr int kBFrags = BN / 16;
-  static constexpr int kBOff = kAFrags * 2048;
+  static constexpr int kBOff = kAFrags * kAFragBytes;
   static constexpr int kStageBytes = kBOff + kBFrags * 1024;
   static constexpr int kWscBytes = WN * kNIBlk * 4;  // weight block scales (after the stages)
-  static constexpr int kStages = 3;
+  static constexpr int kStages = STAGES;
   static_assert(kStages >= 2 && kStages <= 5, "pipeline depth");
   static constexpr int kSteps = kI / 64;  // stages per tile (two per scale block)
-  static constexpr int kPlanes = 2 * kAFrags + kBFrags;
+  static constexpr int kPlanes = kAPlanes + kBFrags;
   static_assert(kPlanes % kWaves == 0, "planes must split evenly over waves");
   static constexpr int kPlanesPerWave = kPlanes / kWaves;
   static constexpr int kGroupM = 4;
 };
 
-template <int WM, int WN, int MI, int NJ>
+template <int WM, int WN, int MI, int NJ, int STAGES>
 __global__ void __launch_bounds__(64 * WM * WN)
 gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
                    const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
-                   uint16_t* __restrict__ down) {
-  using C = G2Tiled<WM, WN, MI, NJ>;
+                   float* __restrict__ down) {
+  using C = G2Tiled<WM, WN, MI, NJ, STAGES>;
   // One LDS object (see gemm1.hip): the stage ring, then the weight scales.
   __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
 
@@ -291,21 +301,24 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
   // MFMA operand slots: A rows in wide layout (chunks 2q, 2q+1), B rows narrow (chunk q)
   const int slot_a0 = wide_slot(lr, 2 * lq), slot_a1 = wide_slot(lr, 2 * lq + 1), slot_b = narrow_slot(lr, lq);
 
-  // per-lane DMA sources at stage 0 (byte pointers) and LDS destinations
+  // per-lane DMA sources at stage 0 (byte pointers) and LDS destinations.
+  // A plane 4f + 2h + p: rows 8p .. 8p+7 of row block f, hi (h = 0) or lo
+  // (h = 1) half of the stage's 64 columns (128 bytes each, adjacent in the
+  // act row).
   const char* src[C::kPlanesPerWave];
   int dst[C::kPlanesPerWave];
 #pragma unroll
   for (int k = 0; k < C::kPlanesPerWave; ++k) {
     const int plane = wave + k * C::kWaves;
-    if (plane < 2 * C::kAFrags) {
-      const int f = plane >> 1, p = plane & 1;
+    if (plane < C::kAPlanes) {
+      const int f = plane >> 2, h = (plane >> 1) & 1, p = plane & 1;
       int fr, chunk;
       wide_copy_lane(lane, p, fr, chunk);
       const int r = min(f * 16 + fr, rows - 1);
-      src[k] = (const char*)(act + (size_t)(row0 + r) * kI + 8 * chunk);
-      dst[k] = f * 2048 + p * 1024;
+      src[k] = (const char*)(act + (size_t)(row0 + r) * kActRowElems) + 128 * h + 16 * chunk;
+      dst[k] = f * C::kAFragBytes + h * 2048 + p * 1024;
     } else {
-      const int f = plane - 2 * C::kAFrags;
+      const int f = plane - C::kAPlanes;
       int fr, chunk;
       narrow_copy_lane(lane, fr, chunk);
       src[k] = (const char*)(w2 + ((size_t)e * kH + n0 + 16 * f + fr) * kI + 16 * chunk);
@@ -316,7 +329,7 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
     char* base = lds + (s % C::kStages) * C::kStageBytes;
 #pragma unroll
     for (int k = 0; k < C::kPlanesPerWave; ++k) {
-      const int step = (dst[k] < C::kBOff) ? s * 64 * 2 : s * 64;  // bytes per stage: bf16 A, e4m3 B
+      const int step = (dst[k] < C::kBOff) ? s * 256 : s * 64;  // bytes per stage: bf16 hi + lo A, e4m3 B
       dma16(src[k] + step, base + dst[k]);
     }
   };
@@ -343,12 +356,14 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
     if (s + C::kStages - 1 < C::kSteps) issue(s + C::kStages - 1);
 
     const char* sbuf = lds + (s % C::kStages) * C::kStageBytes;
-    v8bf a[MI][2], b[NJ][2];
+    v8bf a[MI][2], al[MI][2], b[NJ][2];
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      const char* f = sbuf + (wm * MI + mi) * 2048;
+      const char* f = sbuf + (wm * MI + mi) * C::kAFragBytes;
       a[mi][0] = *(const v8bf*)(f + slot_a0);
       a[mi][1] = *(const v8bf*)(f + slot_a1);
+      al[mi][0] = *(const v8bf*)(f + 2048 + slot_a0);
+      al[mi][1] = *(const v8bf*)(f + 2048 + slot_a1);
     }
 #pragma unroll
     for (int nj = 0; nj < NJ; ++nj) {
@@ -362,6 +377,8 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
       for (int nj = 0; nj < NJ; ++nj) {
         P[mi][nj] = mfma_bf16_16x16x32(a[mi][0], b[nj][0], P[mi][nj]);
         P[mi][nj] = mfma_bf16_16x16x32(a[mi][1], b[nj][1], P[mi][nj]);
+        P[mi][nj] = mfma_bf16_16x16x32(al[mi][0], b[nj][0], P[mi][nj]);
+        P[mi][nj] = mfma_bf16_16x16x32(al[mi][1], b[nj][1], P[mi][nj]);
       }
     if (s & 1) {
       const float sb = wsc[wn * kNIBlk + (s >> 1)];
@@ -383,32 +400,33 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = (wm * MI + mi) * 16 + 4 * lq + i;
-        if (r < rows)
-          down[(size_t)(row0 + r) * kH + n0 + 16 * (wn * NJ + nj) + lr] = f32_to_bf16_rne(acc[mi][nj][i]);
+        if (r < rows) down[(size_t)(row0 + r) * kH + n0 + 16 * (wn * NJ + nj) + lr] = acc[mi][nj][i];
       }
 }
 
-template <int WM, int WN, int MI, int NJ>
+template <int WM, int WN, int MI, int NJ, int STAGES>
 hipError_t launch_gemm2_tiled(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
                               hipStream_t stream) {
-  using C = G2Tiled<WM, WN, MI, NJ>;
+  using C = G2Tiled<WM, WN, MI, NJ, STAGES>;
   const int64_t pairs = (int64_t)T * kTopK;
   const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
   const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
-  hipLaunchKernelGGL((gemm2_tiled_kernel<WM, WN, MI, NJ>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
+  hipLaunchKernelGGL((gemm2_tiled_kernel<WM, WN, MI, NJ, STAGES>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
                      stream, (const uint16_t*)(ws + L.act), w2, w2_scale,
-                     (const int32_t*)(ws + L.expert_off), (uint16_t*)(ws + L.down));
+                     (const int32_t*)(ws + L.expert_off), (float*)(ws + L.down));
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// Wide path (large T): 256 rows x 256 columns per workgroup, for the same
-// reason as GEMM1's wide path -- the L2 -> LDS copy rate per CU, not the
-// MFMAs, bounds the 128 x 256 tiles, and a 256 x 256 tile copies 48 KB instead
-// of 64 KB per 8.4 MFLOP.
+// Wide path (large T): 128 rows x 256 columns per workgroup.  Each row carries
+// its activation as a hi and a lo bf16 plane, so a 64-K stage holds
+// 128 x 256 B of activation and 256 x 64 B of W2 (48 KB), and multiplying it
+// takes as many MFMAs as a 256 x 256 tile of single bf16 rows.  The L2 -> LDS
+// copy rate per CU, not the MFMAs, bounds narrower tiles.
 //
-//   * 8 waves as 4 (rows) x 2 (columns); wave tile 64 rows x 128 columns (one
-//     128-column weight scale block), 4 x 8 MFMA blocks, 128 accumulator VGPRs;
+//   * 8 waves as 4 (rows) x 2 (columns); wave tile 32 rows x 128 columns (one
+//     128-column weight scale block), 2 x 8 MFMA blocks of four MFMAs each
+//     (hi and lo, two 32-K halves), 64 accumulator VGPRs;
 //   * the scale is applied per 64-K stage (acc += P_stage * w_scale[n/128,
 //     k/128]), so no second set of block partials stays live across stages;
 //   * three 48 KB LDS stages, the copies of stages s+1 and s+2 in flight while
@@ -417,29 +435,32 @@ hipError_t launch_gemm2_tiled(int T, const uint8_t* w2, const float* w2_scale, c
 struct G2Wide {
   static constexpr int kWaves = 8;
   static constexpr int kThreads = kWave * kWaves;
-  static constexpr int WM = 4, WN = 2, MI = 4, NJ = 8;
-  static constexpr int BM = 16 * MI * WM;  // 256
+  static constexpr int WM = 4, WN = 2, MI = 2, NJ = 8;
+  static constexpr int BM = 16 * MI * WM;  // 128
   static constexpr int BN = 16 * NJ * WN;  // 256
   static constexpr int kNT = kH / BN;      // 28
   static_assert(kH % BN == 0 && 16 * NJ == kBlk, "a wave's columns are one scale block");
   static constexpr int kAFrags = BM / 16;
+  static constexpr int kAFragBytes = 4096;  // hi (two wide planes), then lo (two wide planes)
+  static constexpr int kAPlanes = 4 * kAFrags;
   static constexpr int kBFrags = BN / 16;
-  static constexpr int kBOff = kAFrags * 2048;
+  static constexpr int kBOff = kAFrags * kAFragBytes;
   static constexpr int kStageBytes = kBOff + kBFrags * 1024;  // 48 KB
   static constexpr int kStages = 3;
   static constexpr int kWscBytes = WN * kNIBlk * 4;
   static constexpr int kSteps = kI / 64;
-  static constexpr int kPlanes = 2 * kAFrags + kBFrags;
+  static constexpr int kPlanes = kAPlanes + kBFrags;
   static constexpr int kPlanesPerWave = kPlanes / kWaves;  // 6: 4 A + 2 B
+  static constexpr int kAPlanesPerWave = kAPlanes / kWaves;
   static constexpr int kGroupM = 4;
-  static_assert(kPlanes % kWaves == 0 && (2 * kAFrags) % kWaves == 0, "planes split evenly");
+  static_assert(kPlanes % kWaves == 0 && kAPlanes % kWaves == 0, "planes split evenly");
   static_assert(kStages * kStageBytes + kWscBytes <= 160 * 1024, "LDS");
 };
 
 __global__ void __launch_bounds__(G2Wide::kThreads)
 gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
                   const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
-                  uint16_t* __restrict__ down) {
+                  float* __restrict__ down) {
   using C = G2Wide;
   __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
 
@@ -463,23 +484,25 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
   // MFMA operand slots: A rows in wide layout (chunks 2q, 2q+1), B rows narrow (chunk q)
   const int slot_a0 = wide_slot(lr, 2 * lq), slot_a1 = wide_slot(lr, 2 * lq + 1), slot_b = narrow_slot(lr, lq);
 
-  // DMA planes wave + 8k: k < 4 are A planes (bf16 act rows), k >= 4 B planes
-  const char* actb = (const char*)(act + (size_t)row0 * kI);
+  // DMA planes wave + 8k: k < 4 are A planes (act rows), k >= 4 B planes.
+  // A plane 4f + 2h + p: rows 8p .. 8p+7 of row block f, hi (h = 0) or lo
+  // (h = 1) half of the stage's 64 columns (adjacent 128-byte runs of the row).
+  const char* actb = (const char*)(act + (size_t)row0 * kActRowElems);
   const uint8_t* w2e = w2 + (size_t)e * kH * kI;
   uint32_t off[C::kPlanesPerWave];
   int dst[C::kPlanesPerWave];
 #pragma unroll
   for (int k = 0; k < C::kPlanesPerWave; ++k) {
     const int plane = wave + k * C::kWaves;
-    if (plane < 2 * C::kAFrags) {
-      const int f = plane >> 1, p = plane & 1;
+    if (plane < C::kAPlanes) {
+      const int f = plane >> 2, h = (plane >> 1) & 1, p = plane & 1;
       int fr, chunk;
       wide_copy_lane(lane, p, fr, chunk);
       const int r = min(f * 16 + fr, rows - 1);
-      off[k] = (uint32_t)(r * kI + 8 * chunk) * 2;
-      dst[k] = f * 2048 + p * 1024;
+      off[k] = (uint32_t)(r * kActRowElems * 2 + 128 * h + 16 * chunk);
+      dst[k] = f * C::kAFragBytes + h * 2048 + p * 1024;
     } else {
-      const int f = plane - 2 * C::kAFrags;
+      const int f = plane - C::kAPlanes;
       int fr, chunk;
       narrow_copy_lane(lane, fr, chunk);
       off[k] = (uint32_t)(n0 + 16 * f + fr) * kI + 16 * chunk;
@@ -488,14 +511,14 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
   }
   auto issue = [&](int s) {
     char* base = lds + (s % C::kStages) * C::kStageBytes;
-    const char* ak = actb + s * 64 * 2;
+    const char* ak = actb + s * 256;
     const uint8_t* wk = w2e + s * 64;
 #pragma unroll
     for (int k = 0; k < C::kPlanesPerWave; ++k) {
-      const bool a_plane = k < 2 * C::kAFrags / C::kWaves;
+      const bool a_plane = k < C::kAPlanesPerWave;
       // A fragments wholly past the tile's rows are never read: no copy
       if (a_plane) {
-        if (((wave + k * C::kWaves) >> 1) * 16 < rows) dma16(ak + off[k], base + dst[k]);
+        if (((wave + k * C::kWaves) >> 2) * 16 < rows) dma16(ak + off[k], base + dst[k]);
       } else {
         dma16(wk + off[k], base + dst[k]);
       }
@@ -520,12 +543,14 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
     // first MFMAs wait only for their own operands
     v4i braw[C::NJ];
     braw[0] = bread(0);
-    v8bf a[C::MI][2];
+    v8bf a[C::MI][2], al[C::MI][2];
 #pragma unroll
     for (int mi = 0; mi < C::MI; ++mi) {
-      const char* f = sbuf + (wm * C::MI + mi) * 2048;
+      const char* f = sbuf + (wm * C::MI + mi) * C::kAFragBytes;
       a[mi][0] = *(const v8bf*)(f + slot_a0);
       a[mi][1] = *(const v8bf*)(f + slot_a1);
+      al[mi][0] = *(const v8bf*)(f + 2048 + slot_a0);
+      al[mi][1] = *(const v8bf*)(f + 2048 + slot_a1);
     }
     braw[1] = bread(1);
     const float sb = wsc[wn * kNIBlk + (s >> 1)];
@@ -540,12 +565,14 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
       const v8bf b0 = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
       const v8bf b1 = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
       // operands swapped (W2 rows as the MFMA's A): lane (q, r) receives
-      // row r, columns 4q .. 4q+3 of the block, stored as one 8-byte write
+      // row r, columns 4q .. 4q+3 of the block, stored as one 16-byte write
       v4f pc[C::MI];
 #pragma unroll
       for (int mi = 0; mi < C::MI; ++mi) {
         pc[mi] = mfma_bf16_16x16x32(b0, a[mi][0], v4f{0.f, 0.f, 0.f, 0.f});
         pc[mi] = mfma_bf16_16x16x32(b1, a[mi][1], pc[mi]);
+        pc[mi] = mfma_bf16_16x16x32(b0, al[mi][0], pc[mi]);
+        pc[mi] = mfma_bf16_16x16x32(b1, al[mi][1], pc[mi]);
       }
       if (nj > 0) {
 #pragma unroll
@@ -569,7 +596,7 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
   int ops_per_stage = 0;
 #pragma unroll
   for (int k = 0; k < C::kPlanesPerWave; ++k)
-    ops_per_stage += (k >= 2 * C::kAFrags / C::kWaves || ((wave + k * C::kWaves) >> 1) * 16 < rows) ? 1 : 0;
+    ops_per_stage += (k >= C::kAPlanesPerWave || ((wave + k * C::kWaves) >> 2) * 16 < rows) ? 1 : 0;
 
 #pragma unroll
   for (int s = 0; s < C::kStages - 1; ++s) issue(s);
@@ -590,14 +617,9 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
   for (int mi = 0; mi < C::MI; ++mi) {
     const int r = (wm * C::MI + mi) * 16 + lr;
     if (r < rows) {
-      uint16_t* drow = down + (size_t)(row0 + r) * kH + n0 + 16 * wn * C::NJ + 4 * lq;
+      float* drow = down + (size_t)(row0 + r) * kH + n0 + 16 * wn * C::NJ + 4 * lq;
 #pragma unroll
-      for (int nj = 0; nj < C::NJ; ++nj) {
-        uint2 v;
-        v.x = (uint32_t)f32_to_bf16_rne(acc[mi][nj][0]) | ((uint32_t)f32_to_bf16_rne(acc[mi][nj][1]) << 16);
-        v.y = (uint32_t)f32_to_bf16_rne(acc[mi][nj][2]) | ((uint32_t)f32_to_bf16_rne(acc[mi][nj][3]) << 16);
-        *(uint2*)(drow + 16 * nj) = v;
-      }
+      for (int nj = 0; nj < C::NJ; ++nj) *(v4f*)(drow + 16 * nj) = acc[mi][nj];
     }
   }
 }
@@ -610,7 +632,7 @@ hipError_t launch_gemm2_wide(int T, const uint8_t* w2, const float* w2_scale, co
   const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
   hipLaunchKernelGGL(gemm2_wide_kernel, dim3((unsigned)blocks), dim3(C::kThreads), 0, stream,
                      (const uint16_t*)(ws + L.act), w2, w2_scale, (const int32_t*)(ws + L.expert_off),
-                     (uint16_t*)(ws + L.down));
+                     (float*)(ws + L.down));
   return hipGetLastError();
 }
 
@@ -626,7 +648,7 @@ hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const L
                        (const int32_t*)(ws + L.perm_token), (const float*)(ws + L.perm_w), T, (uint16_t*)out);
     return hipGetLastError();
   }
-  if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<2, 4, 2, 4>(T, w2, w2_scale, L, ws, stream);
+  if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<2, 4, 2, 4, 3>(T, w2, w2_scale, L, ws, stream);
   return launch_gemm2_wide(T, w2, w2_scale, L, ws, stream);
 }
 

@@ -36,6 +36,18 @@ static_assert(kMaxTokens * kH <= (int64_t)1 << 32, "token row offsets fit in 32 
 // never reach the workspace, and no combine pass runs.
 constexpr int kGemm2StreamMaxTokens = 64;
 
+// SwiGLU activation rows (`act`) hold each fp32 value v as a pair of bf16,
+// hi = bf16(v) and lo = bf16(v - hi), so hi + lo carries v to ~2^-17
+// relative: GEMM2 multiplies both on bf16 MFMA, as the fp32 activation of the
+// reference (moe.py:190-196) needs -- a single bf16 rounding leaves the
+// output within 1e-2 only while its magnitude stays small.  A row is 32
+// chunks of 64 columns, chunk c = [hi of columns 64c..64c+63][lo of the
+// same], 8 KB per row: one 64-column step of GEMM2 reads 256 contiguous bytes
+// per row.
+constexpr int kActRowElems = 2 * kI;  // bf16 elements per act row
+// Element index of the hi half of column `col` inside an act row (lo at +64).
+__host__ __device__ constexpr int act_col(int col) { return (col >> 6) * 128 + (col & 63); }
+
 struct Layout {
   size_t topk_ids, topk_w, pair_row, expert_off, perm_token, perm_w, act, down, block_hist, total;
 };
@@ -57,9 +69,9 @@ constexpr Layout make_layout(int64_t T) {
   L.pair_row = take(rows * sizeof(int32_t));
   L.perm_token = take(rows * sizeof(int32_t));
   L.perm_w = take(rows * sizeof(float));
-  L.act = take(rows * kI * sizeof(uint16_t));
-  // GEMM2 rows exist only where a separate combine pass reads them
-  L.down = take(T > kGemm2StreamMaxTokens ? rows * kH * sizeof(uint16_t) : 0);
+  L.act = take(rows * kActRowElems * sizeof(uint16_t));
+  // fp32 GEMM2 rows, only where a separate combine pass reads them
+  L.down = take(T > kGemm2StreamMaxTokens ? rows * kH * sizeof(float) : 0);
   L.block_hist = take((size_t)((T + 3) / 4) * kELocal * sizeof(int32_t));  // per route workgroup (4 tokens)
   L.total = off;
   return L;
@@ -123,6 +135,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+
+// v -> (hi, lo) bf16 bits with hi = RNE(v), lo = RNE(v - hi); v - hi is exact
+// in fp32.  Non-finite hi keeps lo = 0, so hi + lo stays inf / NaN like v.
+__device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
+  hi = f32_to_bf16_rne(v);
+  const float h = bf16_to_f32(hi);
+  lo = __builtin_isfinite(h) ? f32_to_bf16_rne(v - h) : (uint16_t)0;
+}
 
 // Order-preserving map of a (non-NaN) float to uint32.
 __device__ __forceinline__ uint32_t float_order_key(float v) {

@@ -170,9 +170,11 @@ class RouteResult:
         self.expert_off = view(lay.expert_off, E_LOCAL + 1, torch.int32)
         self.perm_token = view(lay.perm_token, T * TOP_K, torch.int32)
         self.perm_w = view(lay.perm_w, T * TOP_K, torch.float32)
-        self.act = view(lay.act, T * TOP_K * I, torch.int16).view(T * TOP_K, I)
-        # GEMM2 rows reach the workspace only where a combine pass reads them
-        self.down = (view(lay.down, T * TOP_K * H, torch.int16).view(T * TOP_K, H)
+        # SwiGLU rows as bf16 (hi, lo) pairs: per 64-column chunk, 64 hi then
+        # 64 lo values (act_values() decodes them to fp32 hi + lo)
+        self.act = view(lay.act, T * TOP_K * 2 * I, torch.int16).view(T * TOP_K, 2 * I)
+        # fp32 GEMM2 rows, in the workspace only where a combine pass reads them
+        self.down = (view(lay.down, T * TOP_K * H, torch.float32).view(T * TOP_K, H)
                      if T > FUSED_COMBINE_MAX_TOKENS else None)
         # one row per routing workgroup: 4 tokens each up to T = 1024, 16 beyond
         blocks = (T + 3) // 4 if T <= 1024 else (T + 15) // 16
@@ -191,6 +193,15 @@ def route(routing_logits, routing_bias, local_expert_offset, routed_scaling_fact
     if rc != _lib.OK:
         raise RuntimeError(f"moe_fp8_ds_route: {_lib.status_string(rc)} ({rc})")
     return RouteResult(ws, T)
+
+
+def act_values(act_rows: torch.Tensor) -> torch.Tensor:
+    """fp32 values [n, 2048] of act rows [n, 4096] (int16 bf16 bits, per
+    64-column chunk 64 hi then 64 lo): hi + lo."""
+    n = act_rows.shape[0]
+    bits = act_rows.reshape(n, I // 64, 2, 64).to(torch.int32) & 0xFFFF
+    f = (bits << 16).view(torch.float32)
+    return (f[:, :, 0, :] + f[:, :, 1, :]).reshape(n, I)
 
 
 def intermediates(ws: torch.Tensor, T: int) -> RouteResult:

@@ -44,8 +44,8 @@ def test_layout_regions_disjoint_and_aligned(pkg):
         assert lay.total == L.moe_fp8_ds_workspace_size(T)
         regions = sorted([
             (lay.block_hist, 128 * ((T + 3) // 4)), (lay.expert_off, 256), (lay.topk_ids, 32 * T), (lay.topk_w, 32 * T),
-            (lay.pair_row, 32 * T), (lay.perm_token, 32 * T), (lay.perm_w, 32 * T), (lay.act, 8 * T * 2048 * 2),
-            (lay.down, 8 * T * 7168 * 2 if T > 64 else 0)])
+            (lay.pair_row, 32 * T), (lay.perm_token, 32 * T), (lay.perm_w, 32 * T), (lay.act, 8 * T * 2048 * 4),
+            (lay.down, 8 * T * 7168 * 4 if T > 64 else 0)])
         for (a, na), (b, _) in zip(regions, regions[1:]):
             assert a % 256 == 0 and a + na <= b
         assert regions[-1][0] + regions[-1][1] <= lay.total

@@ -32,31 +32,37 @@ def sample_tokens(ids, off, n, rng, T):
     return np.array(sorted(pick), np.int64)
 
 
+# (config, local_expert_offset override, T override, tokens checked: None = every token)
 LAYER_CASES = [
-    ("plumbing_t16", None, None, 16),
-    ("decode_t1", None, None, 1),
-    ("decode_t1_s3", None, None, 1),
-    ("small_t64", None, None, 64),
-    ("prefill_t1024", None, None, 40),
-    ("skewed_t8192", None, None, 24),
-    ("small_t64", 224, None, 64),
-    ("small_t64", 240, 37, 37),
-    ("small_t64", -16, 21, 21),
-    ("prefill_t1024", 256, 128, 8),
+    ("plumbing_t16", None, None, None),
+    ("decode_t1", None, None, None),
+    ("decode_t1_s3", None, None, None),
+    ("small_t64", None, None, None),
+    ("prefill_t1024", None, None, None),
+    ("skewed_t8192", None, None, None),
+    ("small_t64", 224, None, None),
+    ("small_t64", 240, 37, None),
+    ("small_t64", -16, 21, None),
+    ("prefill_t1024", 256, 128, None),
     # token counts on either side of each kernel-choice boundary
-    ("small_t64", None, 17, 17),        # first T past the in-GEMM1 routing
-    ("prefill_t1024", None, 65, 24),    # first T with the tiled GEMM1 and a combine pass
-    ("skewed_t8192", None, 1024, 16),   # largest T of the tiled GEMM1
-    ("skewed_t8192", None, 1025, 16),   # smallest T of the wide GEMM1
-    ("skewed_t8192", None, 2047, 16),
-    ("skewed_t8192", None, 2048, 16),
-    ("skewed_t8192", None, 4095, 16),   # largest T of the tiled GEMM2
-    ("skewed_t8192", None, 4096, 16),   # smallest T of the wide GEMM2
+    ("small_t64", None, 17, None),        # first T past the in-GEMM1 routing
+    ("prefill_t1024", None, 65, None),    # first T with the tiled GEMM1 and a combine pass
+    ("skewed_t8192", None, 1024, None),   # largest T of the tiled GEMM1
+    ("skewed_t8192", None, 1025, None),   # smallest T of the wide GEMM1
+    ("skewed_t8192", None, 2047, None),
+    ("skewed_t8192", None, 2048, None),
+    ("skewed_t8192", None, 4095, None),   # largest T of the tiled GEMM2
+    ("skewed_t8192", None, 4096, None),   # smallest T of the wide GEMM2
+    # the contest dataset's largest T (moe.py:13), sampled
+    ("skewed_t8192", None, 14107, 768),
 ]
 
 
 @pytest.mark.parametrize("name,offset,T,n_check", LAYER_CASES)
 def test_layer_matches_oracle(pkg, orc, cuda_device, name, offset, T, n_check):
+    """Every checked token whose routed expert ids equal the oracle's is
+    compared element-wise; a token whose ids differ must be a near-tie of the
+    fp32 scores (and is then left out)."""
     cfg = pkg.synth.CONFIGS[name]
     off = cfg.local_expert_offset if offset is None else offset
     w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
@@ -65,18 +71,23 @@ def test_layer_matches_oracle(pkg, orc, cuda_device, name, offset, T, n_check):
     print(f"layer case {name} offset={off} T={T}", flush=True)
     out = run_layer(pkg, tok, w, off, cfg.routed_scaling_factor).float().cpu().numpy()
     assert np.isfinite(out).all(), "output not fully written / non-finite"
+    gpu_ids = pkg.intermediates(pkg.workspace(cuda_device, T), T).topk_ids.cpu().numpy()
 
     ref_ids, _ = orc.route(host[0], host[1], cfg.routed_scaling_factor)
     tie = near_tie_tokens(host[0], host[1], cfg.routed_scaling_factor)
+    differ = (np.sort(gpu_ids, axis=1) != ref_ids).any(axis=1)
+    assert not (differ & ~tie).any(), f"ids differ outside near-ties: tokens {np.nonzero(differ & ~tie)[0][:8]}"
     rng = np.random.default_rng(T)
-    toks = np.arange(T) if T <= n_check else sample_tokens(ref_ids, off, n_check, rng, T)
-    toks = toks[~tie[toks]]
+    toks = np.arange(T) if n_check is None or T <= n_check else sample_tokens(ref_ids, off, n_check, rng, T)
+    toks = toks[~differ[toks]]
     x = oracle_inputs(cfg, host, w_host)
     ref = orc.bf16_to_f32(orc.moe(x, tokens=toks, local_expert_offset=off))
     got = out[toks]
     bad = bf16_close(got, ref)
     err = np.abs(got - ref)
-    print(f"  checked {len(toks)} tokens: max|err| {err.max():.3e}, max|ref| {np.abs(ref).max():.3f}")
+    print(f"  near-tie tokens {int(tie.sum())} (ids differ on {int(differ.sum())}); checked {len(toks)} tokens: "
+          f"max|err| {err.max() if err.size else 0:.3e}, max|ref| {np.abs(ref).max() if ref.size else 0:.3f}, "
+          f"bit-equal {np.mean(got == ref) if ref.size else 1:.4f}")
     assert not bad.any(), f"{int(bad.sum())} elements outside tolerance, worst {err.max()}"
     # tokens without a local expert produce exact zeros
     le = ref_ids - off
@@ -109,8 +120,8 @@ INTERMEDIATE_CASES = [
 
 @pytest.mark.parametrize("name,T,n_rows", INTERMEDIATE_CASES)
 def test_intermediates_match_oracle(pkg, orc, cuda_device, name, T, n_rows):
-    """SwiGLU activation rows (bf16) and GEMM2 rows (fp32) per (token, expert)
-    pair; with n_rows set, a sample that includes every expert's first and last
+    """SwiGLU activation rows (bf16 hi/lo pairs) and GEMM2 rows (fp32) per
+    (token, expert) pair; with n_rows set, a sample that includes every expert's first and last
     row (tile edges)."""
     cfg = pkg.synth.CONFIGS[name]
     w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
@@ -129,16 +140,23 @@ def test_intermediates_match_oracle(pkg, orc, cuda_device, name, T, n_rows):
         edges = np.concatenate([[offs[e], offs[e + 1] - 1] for e in range(32) if offs[e + 1] > offs[e]])
         rng = np.random.default_rng(n)
         sel = np.unique(np.concatenate([edges, rng.choice(n, n_rows, replace=False)]))
-    act = (r.act[sel].cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    act = pkg.moe.act_values(r.act[torch.as_tensor(sel, device=r.act.device)]).cpu().numpy()
     x = oracle_inputs(cfg, host, w_host)
     c_ref, o_ref = orc.expert_rows(x, perm[sel], le_all[sel])
-    bad_c = bf16_close(act, c_ref, atol=1e-3, rtol=1e-2)
+    # act is carried as a bf16 (hi, lo) pair: fp32-level agreement (hi + lo is
+    # within ~2^-17 of the fp32 value; the GEMM's fp32 summation order differs)
+    ec = np.abs(act - c_ref)
+    print(f"  act: max|err| {ec.max():.3e} (max|ref| {np.abs(c_ref).max():.3f}), "
+          f"max rel {np.max(ec / (np.abs(c_ref) + 1e-3)):.3e}")
+    bad_c = bf16_close(act, c_ref, atol=5e-4, rtol=1e-4)
     assert not bad_c.any(), f"act: {int(bad_c.sum())} bad, rows {np.unique(np.nonzero(bad_c)[0])[:8]}"
     if T <= pkg.moe.FUSED_COMBINE_MAX_TOKENS:
         assert r.down is None
         return  # GEMM2 rows are combined in registers, never stored
-    down = (r.down[sel].cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
-    bad_o = bf16_close(down, o_ref, atol=1e-2, rtol=1e-2)
+    down = r.down[torch.as_tensor(sel, device=r.down.device)].cpu().numpy()
+    eo = np.abs(down - o_ref)
+    print(f"  down: max|err| {eo.max():.3e} (max|ref| {np.abs(o_ref).max():.3f})")
+    bad_o = bf16_close(down, o_ref, atol=1e-4, rtol=1e-4)
     assert not bad_o.any(), f"down: {int(bad_o.sum())} bad, rows {np.unique(np.nonzero(bad_o)[0])[:8]}"
 
 

@@ -1,0 +1,60 @@
+"""Layer output at large magnitudes, where the absolute tolerance no longer
+hides the rounding of intermediates.
+
+The contest's own workloads reach output magnitudes of ~5e5
+(moe/solution/cuda/moe.cu:876-880), where an element passes atol = rtol =
+1e-2 only with about 7 significant bits left after cancellation: bf16
+intermediates (act, GEMM2 rows) then fail several percent of the elements.
+The layer carries act as a bf16 (hi, lo) pair and the GEMM2 rows in fp32.
+Outputs are scaled up through hidden_states_scale (the layer is linear in
+it up to SwiGLU, so outputs grow about as its square) and checked against
+the oracle with the verdict driver's check in match-ratio mode, at the
+fraction the reference's CUDA notes record for the harness
+(moe/solution/cuda/moe.cu:1802: 0.998).  The allclose verdict is printed
+beside it.  It cannot be required: GEMM1 runs on the fp8 MFMA, whose block
+sums carry ~2^-15 rms error (tests/test_gpu_mfma_precision.py), so at these
+magnitudes a few elements in 10^5 that cancel to near zero exceed 1%.  The
+torch fp32 restatement of the definition on the GPU (verdict.reference_layer,
+fp32 GEMMs in another summation order) is printed as the floor of an
+implementation without fp8 tensor-core arithmetic."""
+import numpy as np
+import pytest
+import torch
+
+from util import gpu_tokens, gpu_weights, oracle_inputs
+
+pytestmark = pytest.mark.gpu
+
+H = 7168
+
+
+HARNESS_MATCH_RATIO = 0.998  # moe/solution/cuda/moe.cu:1802
+
+
+@pytest.mark.parametrize("factor", [30.0, 300.0])
+def test_large_magnitude_output(pkg, orc, cuda_device, factor):
+    cfg = pkg.synth.CONFIGS["prefill_t1024"]
+    T = 128
+    w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, host = gpu_tokens(pkg, cfg, cuda_device, T)
+    tok = (tok[0], tok[1], tok[2], (tok[3] * factor).contiguous())
+    host = (host[0], host[1], host[2], (host[3] * np.float32(factor)).astype(np.float32))
+    print(f"large-magnitude case factor={factor} T={T}", flush=True)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=cuda_device)
+    pkg.run(*tok, *w, cfg.local_expert_offset, cfg.routed_scaling_factor, out)
+    torch.cuda.synchronize()
+
+    x = oracle_inputs(cfg, host, w_host)
+    ref_bits = orc.moe(x)
+    ref = torch.from_numpy(ref_bits.view(np.int16)).view(torch.bfloat16).to(cuda_device)
+    v = pkg.verdict
+    chk_all = v.check_output(out, ref)
+    chk_ratio = v.check_output(out, ref, required_matched_ratio=HARNESS_MATCH_RATIO)
+    floor = v.check_output(v.reference_layer(*tok, *w, cfg.local_expert_offset, cfg.routed_scaling_factor), ref)
+    mag = ref.float().abs()
+    print(f"  max|ref| {mag.max().item():.4g}, median|ref| {mag.median().item():.4g}; "
+          f"layer: matched {chk_all.matched_ratio:.6f} ({chk_all.status} allclose, {chk_ratio.status} at "
+          f"{HARNESS_MATCH_RATIO}), "
+          f"max|err| {chk_all.max_abs_err:.4g}; torch fp32 floor: matched {floor.matched_ratio:.6f} ({floor.status})")
+    assert mag.max().item() > 10 * factor  # the scaling did reach large magnitudes
+    assert chk_ratio.status == v.PASSED
