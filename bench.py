@@ -1,16 +1,21 @@
 """Benchmark of the gfx950 FP8 block-scale MoE layer
 `moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048` on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu] [--no-peaks]
 
 A step is one call of the layer (routing, permutation, GEMM1 + SwiGLU, GEMM2,
 combine) on one batch of synthetic inputs already resident in HBM.  The
 headline workload is timed for exactly K steps between two device
-synchronisations; every workload in the sweep is additionally timed as the
-reference harness does (moe/scripts/run_local.py:33: warmup 3, 100 iterations,
-5 trials; the median trial mean is reported) and with per-stage hipEvents on
-the launch stream.  Expert weights rotate over 4 copies (5.6 GB) so that no
-call finds its weights in the 256 MB MALL / L2 left by the previous one.
+synchronisations.  Every workload in the sweep is also timed
+  * from a captured HIP graph of 8 calls, replayed back to back (the device
+    time of a call, free of the Python launch path -- the per-workload
+    latency),
+  * as the reference harness does (moe/scripts/run_local.py:33: warmup 3,
+    100 Python-launched iterations, 5 trials, median trial mean),
+  * per stage, with hipEvents the library records on its launch stream,
+and its CPU reference is timed once on the host cores.  Expert weights rotate
+over 4 copies (5.6 GB), continuously across every loop, so that no call finds
+its weights in the 256 MB MALL / L2 left by the previous one.
 
 Prints ONE JSON line on stdout (progress goes to stderr).
 """
@@ -51,11 +56,15 @@ def log(*a):
 
 def stage_work(stage, T, n_sel, a_act):
     """(algorithmic bytes, flops, peak FLOP/s) of one launch of a stage."""
+    # bytes: weights and scales once, token rows once, intermediates once each
+    # way (act: bf16 hi + lo = 4 B per value; GEMM2 rows: fp32, or for T <= 64
+    # the bf16 output written by GEMM2 itself)
     if stage == "gemm1_swiglu":
-        return (a_act * G1_BYTES_PER_EXPERT + T * (H + 56 * 4) + n_sel * I * 2,
+        return (a_act * G1_BYTES_PER_EXPERT + T * (H + 56 * 4) + n_sel * I * 4,
                 n_sel * G1_FLOPS_PER_PAIR, PEAK["fp8"])
     if stage == "gemm2":
-        return (a_act * G2_BYTES_PER_EXPERT + n_sel * I * 2 + n_sel * H * 4,
+        rows_out = T * H * 2 if T <= 64 else n_sel * H * 4
+        return (a_act * G2_BYTES_PER_EXPERT + n_sel * I * 4 + rows_out,
                 n_sel * G2_FLOPS_PER_PAIR, PEAK["bf16"])
     if stage == "route":
         return (T * 256 * 4 + 512 + T * TOP_K * 16, 0, None)
@@ -85,11 +94,13 @@ class Workload:
         self.w = weights_cache[seed]
         self.tok = pkg.synth.tokens(self.cfg, dev)
         self.out = torch.empty((self.T, H), dtype=torch.bfloat16, device=dev)
+        self.k = 0  # calls so far: the weight copy rotates with every call, across all loops
 
-    def call(self, i, events=None):
+    def call(self, events=None):
         c = self.cfg
-        self.pkg.run(*self.tok, *self.w[i % len(self.w)], c.local_expert_offset, c.routed_scaling_factor,
-                     self.out, stage_events=events)
+        w = self.w[self.k % len(self.w)]
+        self.k += 1
+        self.pkg.run(*self.tok, *w, c.local_expert_offset, c.routed_scaling_factor, self.out, stage_events=events)
 
     def counts(self):
         ws = self.pkg.workspace(self.out.device, self.T)
@@ -100,31 +111,63 @@ class Workload:
 
 
 def time_steps(torch, wl, steps, warmup):
-    for i in range(warmup):
-        wl.call(i)
+    for _ in range(warmup):
+        wl.call()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        wl.call(i)
+    for _ in range(steps):
+        wl.call()
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def harness_protocol(torch, wl, iters, trials, warmup):
-    """hipEvent-timed trials on the launch stream; returns (median trial mean ms, all)."""
+    """hipEvent-timed trials of Python-launched calls on the launch stream;
+    returns (median trial mean ms, all)."""
     s = torch.cuda.current_stream()
-    for i in range(warmup):
-        wl.call(i)
+    for _ in range(warmup):
+        wl.call()
     means = []
     for _ in range(trials):
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record(s)
-        for i in range(iters):
-            wl.call(i)
+        for _ in range(iters):
+            wl.call()
         b.record(s)
         b.synchronize()
         means.append(a.elapsed_time(b) / iters)
+    means.sort()
+    return means[len(means) // 2], means
+
+
+GRAPH_CALLS = 2 * WEIGHT_COPIES  # calls per captured graph: every weight copy twice
+
+
+def graph_latency(torch, wl, replays, trials):
+    """Device time of one call: GRAPH_CALLS calls (rotating weight copies)
+    captured in one HIP graph, replayed `replays` times back to back between
+    two events; returns (median over trials of ms per call, all trials)."""
+    for _ in range(2 * WEIGHT_COPIES):
+        wl.call()  # warm: first-use set-up of every copy outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(GRAPH_CALLS):
+            wl.call()
+    graph.replay()
+    torch.cuda.synchronize()
+    means = []
+    for _ in range(trials):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(replays):
+            graph.replay()
+        b.record()
+        b.synchronize()
+        means.append(a.elapsed_time(b) / (replays * GRAPH_CALLS))
+    del graph
     means.sort()
     return means[len(means) // 2], means
 
@@ -136,7 +179,7 @@ def stage_times(pkg, torch, wl, iters):
     pool = pkg._lib.EventPool(nst * iters)
     try:
         for i in range(iters):
-            wl.call(i, events=pool.ptr(i * nst))
+            wl.call(events=pool.ptr(i * nst))
         torch.cuda.synchronize()
         tot = [0.0] * len(STAGES)
         for i in range(iters):
@@ -147,14 +190,39 @@ def stage_times(pkg, torch, wl, iters):
         pool.close()
 
 
+def near_tie_count(torch, logits, bias, ulps=8):
+    """Tokens whose selection boundary (4th vs 5th group score, 8th vs 9th
+    expert score among the kept groups) lies within `ulps` fp32 ulps: there
+    the expert ids may legitimately differ from the reference's (BASELINE.md
+    asks for the count).  fp32 torch on the inputs' device."""
+    x = logits.float()
+    s = 1.0 / (1.0 + torch.exp(-x))
+    sb = s + bias.float().reshape(1, -1)
+    T = x.shape[0]
+    top2 = sb.view(T, 8, 32).topk(2, dim=2).values.sum(dim=2)
+    gs = top2.sort(dim=1, descending=True).values
+
+    def ulp(v):
+        v = v.abs()
+        return torch.nextafter(v, torch.full_like(v, float("inf"))) - v
+
+    near_g = (gs[:, 3] - gs[:, 4]) <= ulps * ulp(gs[:, 3])
+    keep = torch.zeros_like(top2, dtype=torch.bool).scatter_(1, top2.topk(4, dim=1).indices, True)
+    cand = sb.masked_fill(~keep.repeat_interleave(32, dim=1), float("-inf"))
+    cs = cand.topk(9, dim=1).values
+    near_e = (cs[:, 7] - cs[:, 8]) <= ulps * ulp(cs[:, 7])
+    return int((near_g | near_e).sum().item())
+
+
 def measure(pkg, torch, wl, iters, trials, warmup):
-    med, trials_ms = harness_protocol(torch, wl, iters, trials, warmup)
+    g_ms, g_trials = graph_latency(torch, wl, replays=max(1, iters // GRAPH_CALLS), trials=trials)
+    h_ms, h_trials = harness_protocol(torch, wl, iters, trials, warmup)
     st = stage_times(pkg, torch, wl, min(iters, 50))
     n_sel, a_act = wl.counts()
     T = wl.T
     B = a_act * BYTES_PER_EXPERT + T * BYTES_PER_TOKEN + BYTES_BIAS
     F = n_sel * FLOPS_PER_PAIR
-    sec = med * 1e-3
+    sec = g_ms * 1e-3
     layer = roofline(B, F, PEAK["fp8"], sec)
     dom = max(STAGES, key=lambda k: st[k])
     kb, kf, kp = stage_work(dom, T, n_sel, a_act)
@@ -162,8 +230,10 @@ def measure(pkg, torch, wl, iters, trials, warmup):
     kern.update({"kernel": dom, "ms": st[dom], "algo_bytes": kb, "algo_flops": kf})
     return {
         "workload": wl.name, "T": T, "local_expert_offset": wl.cfg.local_expert_offset, "seed": wl.cfg.seed,
-        "n_sel": n_sel, "a_act": a_act, "latency_us": med * 1e3,
-        "trial_means_us": [round(x * 1e3, 3) for x in trials_ms],
+        "n_sel": n_sel, "a_act": a_act, "near_tie_tokens": near_tie_count(torch, wl.tok[0], wl.tok[1]),
+        "latency_us": g_ms * 1e3, "latency_source": f"graph replay ({GRAPH_CALLS} calls per graph)",
+        "graph_trial_us": [round(x * 1e3, 3) for x in g_trials],
+        "harness_us": h_ms * 1e3, "harness_trial_us": [round(x * 1e3, 3) for x in h_trials],
         "tflops": F / sec / 1e12, "gbps": B / sec / 1e9,
         "bound": layer["bound"], "roofline_frac": layer["frac"],
         "stage_us": {k: round(v * 1e3, 3) for k, v in st.items()},
@@ -175,7 +245,7 @@ def measured_traffic(workload, stage):
     """HBM bytes per launch of `stage` on `workload` from the committed rocprofv3
     counter summaries (profiles/*.txt lines 'TRAFFIC stage=S workload=W
     fetch_bytes=F write_bytes=B', already scaled by the copy calibration), or
-    None when no summary covers it."""
+    None when no summary covers it.  Returns (bytes, file name)."""
     import glob
 
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.txt"))):
@@ -184,8 +254,8 @@ def measured_traffic(workload, stage):
                 continue
             kv = dict(tok.split("=", 1) for tok in line.split()[1:] if "=" in tok)
             if kv.get("stage") == stage and kv.get("workload") == workload:
-                return int(kv["fetch_bytes"]) + int(kv["write_bytes"])
-    return None
+                return int(kv["fetch_bytes"]) + int(kv["write_bytes"]), os.path.relpath(path, ROOT)
+    return None, None
 
 
 def copy_calibration(torch, dev, mib):
@@ -200,16 +270,17 @@ def copy_calibration(torch, dev, mib):
     log(f"[bench] copy calibration: {n} bytes read + {n} bytes written per copy, 3 copies")
 
 
-def cpu_baseline(pkg, torch, wl, budget_tokens):
-    """The oracle (plain-C restatement of full-agent-pipeline/references/moe.py,
-    including its dequantise-all-32-experts step, moe.py:107-118) on the host
-    cores, on two token prefixes of the workload; a linear fit in routed pairs
-    extrapolates to the whole workload."""
+def cpu_time(pkg, torch, wl):
+    """One call of the CPU reference on the whole workload, timed on the host
+    cores: the oracle, a plain-C restatement of
+    full-agent-pipeline/references/moe.py including its
+    dequantise-all-32-experts step (moe.py:107-118), OpenMP over the host's
+    threads.  Returns (seconds, threads)."""
     import numpy as np
 
     from oracle import oracle as orc
 
-    orc.lib()
+    L = orc.lib()
     cfg = wl.cfg
     w = wl.w[0]
     host_w = (w[0].view(torch.uint8).cpu().numpy(), w[1].cpu().numpy(), w[2].view(torch.uint8).cpu().numpy(),
@@ -219,27 +290,54 @@ def cpu_baseline(pkg, torch, wl, budget_tokens):
               tok[2].view(torch.uint8).cpu().numpy(), tok[3].cpu().numpy())
     x = orc.Inputs(*host_t, *host_w, orc.Config(cfg.name, cfg.T, cfg.local_expert_offset, cfg.seed,
                                                  cfg.hot_experts, cfg.hot_add, cfg.routed_scaling_factor))
-    ids, _ = orc.route(host_t[0], host_t[1], cfg.routed_scaling_factor)
-    le = ids - cfg.local_expert_offset
-    local = (le >= 0) & (le < E_LOCAL)
-    pairs_total = int(local.sum())
-    pts = []
-    for n in (budget_tokens, 2 * budget_tokens):
-        toks = np.arange(min(n, cfg.T), dtype=np.int32)
-        t0 = time.perf_counter()
-        orc.moe(x, tokens=toks, dequant_all=True)
-        dt = time.perf_counter() - t0
-        pts.append((int(local[toks].sum()), dt))
-        log(f"[bench] cpu oracle: {len(toks)} tokens, {pts[-1][0]} pairs, {dt:.2f}s")
-    (p1, t1), (p2, t2) = pts
-    slope = (t2 - t1) / max(p2 - p1, 1)
-    est = t1 + slope * (pairs_total - p1)
-    return {
-        "value": est * 1e6, "unit": "us", "cores": orc.lib().orc_num_threads(), "kind": "port",
-        "sample": (f"oracle (C restatement of moe.py incl. dequantise-all-experts) on tokens [0,{budget_tokens}) "
-                   f"and [0,{2 * budget_tokens}) of {cfg.name} ({p1} / {p2} routed pairs: {t1:.2f} s / {t2:.2f} s); "
-                   f"linear fit in pairs extrapolated to all {pairs_total} pairs"),
-    }
+    t0 = time.perf_counter()
+    orc.moe(x, dequant_all=True)
+    dt = time.perf_counter() - t0
+    log(f"[bench] cpu reference {cfg.name}: T={cfg.T} {dt:.2f} s on {L.orc_num_threads()} threads")
+    return dt, L.orc_num_threads()
+
+
+def measured_peaks(pkg, torch, dev):
+    """Roofline denominators measured on this GPU: a streaming read of 4 GiB
+    (16-byte loads, every byte once) and MFMA loops of the two instructions
+    the GEMMs use (operands in registers, 8 waves per CU)."""
+    import ctypes
+
+    L = pkg._lib.bench_lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+
+    def timed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            best = min(best, a.elapsed_time(b) * 1e-3)
+        return best
+
+    nbytes = 4 << 30
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
+    blocks = cus * 16
+    sink = torch.empty(blocks * 512, dtype=torch.float32, device=dev)
+    rd = timed(lambda: L.moe_bench_read_stream(ctypes.c_void_p(buf.data_ptr()), nbytes,
+                                               ctypes.c_void_p(sink.data_ptr()), blocks, stream))
+    del buf
+    out = {"hbm_read_GBps": round(nbytes / rd / 1e9, 1)}
+    for kind, name, k in ((0, "mfma_fp8_TFLOPs", 128), (1, "mfma_bf16_TFLOPs", 32)):
+        iters = 4000
+        t = timed(lambda: L.moe_bench_mfma_loop(kind, iters, cus, ctypes.c_void_p(sink.data_ptr()), stream))
+        flops = cus * 8 * iters * 8 * 2 * 16 * 16 * k
+        out[name] = round(flops / t / 1e12, 1)
+    out["method"] = ("streaming read of 4 GiB with 16-byte loads; MFMA loops of v_mfma_f32_16x16x128_f8f6f4 / "
+                     "v_mfma_f32_16x16x32_bf16, 8 independent accumulators per wave, 8 waves per CU "
+                     "(lib/libmoe_bench.so, csrc/peaks.hip)")
+    log(f"[bench] measured peaks: {out}")
+    return out
 
 
 def measure_quantizer(pkg, torch, dev, T, iters=100):
@@ -287,14 +385,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=GPU_WORKLOADS)
     ap.add_argument("--sweep", default=",".join(GPU_WORKLOADS),
-                    help="comma-separated workloads timed with the harness protocol ('' = none)")
+                    help="comma-separated workloads timed per workload ('' = none)")
     ap.add_argument("--iters", type=int, default=100)
     ap.add_argument("--trials", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-tokens", type=int, default=1024)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU reference timings")
     ap.add_argument("--no-quant", action="store_true", help="skip the activation-quantiser measurement")
+    ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak microbenchmarks")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this size (for PMC byte calibration)")
+    ap.add_argument("--calls-only", action="store_true",
+                    help="only the headline's plain calls (no graphs, no events): for rocprofv3 --pmc runs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -311,18 +411,27 @@ def main():
     cache = {}
 
     sweep = [s for s in args.sweep.split(",") if s]
-    results = {}
+    results, wls = {}, {}
     for name in sweep:
-        wl = Workload(pkg, torch, name, dev, cache)
+        wl = wls[name] = Workload(pkg, torch, name, dev, cache)
         log(f"[bench] {name}: T={wl.T}")
         results[name] = measure(pkg, torch, wl, args.iters, args.trials, args.warmup)
         r = results[name]
-        log(f"[bench] {name}: {r['latency_us']:.1f} us, n_sel={r['n_sel']} a_act={r['a_act']} "
-            f"{r['tflops']:.1f} TFLOP/s {r['gbps']:.0f} GB/s frac={r['roofline_frac']:.3f} stages={r['stage_us']}")
+        log(f"[bench] {name}: {r['latency_us']:.1f} us (graph; harness protocol {r['harness_us']:.1f} us), "
+            f"n_sel={r['n_sel']} a_act={r['a_act']} near-ties={r['near_tie_tokens']} {r['tflops']:.1f} TFLOP/s "
+            f"{r['gbps']:.0f} GB/s frac={r['roofline_frac']:.3f} stages={r['stage_us']}")
 
-    head = Workload(pkg, torch, args.workload, dev, cache)
+    head = wls.get(args.workload) or Workload(pkg, torch, args.workload, dev, cache)
     ms = time_steps(torch, head, args.steps, args.warmup)
     log(f"[bench] headline {args.workload}: {ms * 1e3:.1f} us/step over {args.steps} steps")
+    if args.calls_only:
+        if args.copy_calib_mib:
+            copy_calibration(torch, dev, args.copy_calib_mib)
+        print(json.dumps({"metric": "MoE layer latency (us) (calls only, for counter runs)", "value": round(ms * 1e3, 3),
+                          "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": round(ms, 5), "higher_is_better": False,
+                          "config": {"workload": args.workload}}), flush=True)
+        return
     hm = results.get(args.workload) or measure(pkg, torch, head, args.iters, args.trials, args.warmup)
 
     if args.copy_calib_mib:
@@ -333,25 +442,53 @@ def main():
             quant[f"t{Tq}"] = measure_quantizer(pkg, torch, dev, Tq)
             log(f"[bench] quantize_hidden T={Tq}: {quant[f't{Tq}']['latency_us']:.1f} us "
                 f"{quant[f't{Tq}']['gbps']:.0f} GB/s")
+    peaks = None if args.no_peaks else measured_peaks(pkg, torch, dev)
+
+    cpu = None
+    if not args.no_cpu:
+        for name, wl in list(wls.items()) + ([] if args.workload in wls else [(args.workload, head)]):
+            sec, threads = cpu_time(pkg, torch, wl)
+            if name in results:
+                results[name]["cpu_us"] = sec * 1e6
+                results[name]["speedup_vs_cpu"] = sec * 1e6 / results[name]["latency_us"]
+            if name == args.workload:
+                cpu = {"value": round(sec * 1e6, 1), "unit": "us", "cores": threads, "kind": "port",
+                       "sample": (f"one call of the oracle (plain-C restatement of "
+                                  f"full-agent-pipeline/references/moe.py incl. its dequantise-all-32-experts "
+                                  f"step) on the whole {name} workload (all {wl.T} tokens), OpenMP over "
+                                  f"{threads} host threads; measured, not extrapolated")}
 
     dom = hm["dominant"]
+    traffic, traffic_src = measured_traffic(args.workload, dom["kernel"])
     roof = {"bound": dom["bound"], "achieved": round(dom["achieved"], 3), "peak": dom["peak"],
-            "unit": dom["unit"], "frac": round(dom["frac"], 4),
-            "traffic": measured_traffic(args.workload, dom["kernel"]),
+            "unit": dom["unit"], "frac": round(dom["frac"], 4), "traffic": traffic,
+            "traffic_source": (f"{traffic_src}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run of this bench, "
+                               f"copy-calibrated (not measured in this run)") if traffic_src else None,
             "kernel": dom["kernel"], "kernel_us": round(dom["ms"] * 1e3, 3)}
-    cpu = None if args.no_cpu else cpu_baseline(pkg, torch, head, args.cpu_tokens)
+    if dom["kernel"] == "gemm2":
+        # the activation enters as a bf16 (hi, lo) pair: two bf16 MFMAs per product
+        roof["mfma_flops_executed"] = 2 * dom["algo_flops"]
+        roof["executed_frac"] = round(2 * dom["frac"], 4)
+    if peaks:
+        key = {"GB/s": "hbm_read_GBps", "TFLOP/s": "mfma_bf16_TFLOPs" if dom["kernel"] == "gemm2" else "mfma_fp8_TFLOPs"}
+        roof["peak_measured"] = peaks[key[dom["unit"]]]
+        roof["frac_of_measured_peak"] = round(dom["achieved"] / peaks[key[dom["unit"]]], 4)
 
     line = {
         "metric": "MoE layer latency (us) + FP8 TFLOPS / HBM GB/s as % roofline, T=1..8192",
         "value": round(ms * 1e3, 3), "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp8", "dtype_detail": "e4m3 x e4m3 MFMA (GEMM1), bf16 MFMA (GEMM2), fp32 accumulate", "data": "synthetic (seeded generator)",
+        "dtype": "fp8",
+        "dtype_detail": ("e4m3 x e4m3 MFMA (GEMM1); bf16 MFMA on the activation's (hi, lo) bf16 pair x e4m3 "
+                         "weights widened exactly (GEMM2); fp32 accumulate, fp32 GEMM2 rows"),
+        "data": "synthetic (seeded generator)",
         "config": {"workload": args.workload, "T": head.T, "local_expert_offset": head.cfg.local_expert_offset,
                    "seed": head.cfg.seed, "hot_experts": list(head.cfg.hot_experts), "hot_bias_add": head.cfg.hot_add,
                    "n_sel": hm["n_sel"], "a_act": hm["a_act"], "parallelism": "single GPU (one EP rank)"},
         "tflops": round(hm["tflops"], 2), "gbps": round(hm["gbps"], 1), "layer_roofline_frac": round(hm["roofline_frac"], 4),
         "roofline": roof,
         "cpu_baseline": cpu,
+        "measured_peaks": peaks,
         "upstream_quantizer": quant or None,
         "per_workload": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                          for k, v in results.items()},

@@ -11,6 +11,7 @@ _DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(_DIR, "lib")
 MOE_LIB = os.path.join(LIB_DIR, "libmoe_fp8_ds.so")
 SYNTH_LIB = os.path.join(LIB_DIR, "libmoe_synth.so")
+BENCH_LIB = os.path.join(LIB_DIR, "libmoe_bench.so")
 
 # moe_fp8_ds_status (include/moe_fp8_ds.h)
 OK, ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP, ERR_ARG, ERR_SCRATCH = 0, -1, -2, -3, -4, -5, -6, -7
@@ -78,6 +79,25 @@ def synth_lib() -> ctypes.CDLL:
             getattr(L, f).restype = ctypes.c_int
         _synth = L
     return _synth
+
+
+_bench = None
+
+
+def bench_lib() -> ctypes.CDLL:
+    """Microbenchmarks for bench.py's measured peaks (csrc/peaks.hip)."""
+    global _bench
+    if _bench is None:
+        _need(BENCH_LIB)
+        import torch  # noqa: F401
+
+        L = ctypes.CDLL(BENCH_LIB)
+        P = ctypes.c_void_p
+        L.moe_bench_read_stream.argtypes = [P, ctypes.c_size_t, P, ctypes.c_int, P]
+        L.moe_bench_mfma_loop.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P]
+        L.moe_bench_read_stream.restype = L.moe_bench_mfma_loop.restype = ctypes.c_int
+        _bench = L
+    return _bench
 
 
 def status_string(rc: int) -> str:

@@ -5,6 +5,7 @@
 produces
     lib/libmoe_fp8_ds.so   the MoE layer (C ABI: include/moe_fp8_ds.h)
     lib/libmoe_synth.so    the synthetic input generator (include/moe_synth.h)
+    lib/libmoe_bench.so    microbenchmarks for bench.py's measured peaks (not the layer)
 
 Every call recompiles.  Objects go to _build/ (not committed); the .so files
 are not committed either but travel with the source tree to the GPU host.
@@ -40,6 +41,7 @@ FLAGS = [
 LIBS = {
     "libmoe_fp8_ds.so": ["route.hip", "gemm1.hip", "gemm2.hip", "combine.hip", "quantize.hip", "moe_api.cpp"],
     "libmoe_synth.so": ["synth.hip"],
+    "libmoe_bench.so": ["peaks.hip"],
 }
 
 

@@ -1,0 +1,93 @@
+// peaks.hip -- microbenchmarks for the measured roofline denominators that
+// bench.py reports beside MI355X's published peaks (not part of the layer;
+// built into lib/libmoe_bench.so):
+//   * streaming read: every byte of a buffer read once with 16-byte loads
+//     (what the layer's HBM-bound kernels do with the expert weights);
+//   * MFMA issue rate: independent accumulator chains of the two instructions
+//     the GEMMs use (v_mfma_f32_16x16x128_f8f6f4 and v_mfma_f32_16x16x32_bf16),
+//     operands in registers, 8 waves per CU.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kChains = 8;
+
+// Grid-stride read of n 16-byte words; the xor keeps the loads live and is
+// written once per thread.
+__global__ void __launch_bounds__(256) read_stream(const v4u* __restrict__ src, size_t n, uint32_t* __restrict__ sink) {
+  v4u x = {0u, 0u, 0u, 0u};
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n; i += 4 * stride) {
+    const v4u a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+    x ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n; i += stride) x ^= src[i];
+  sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = x[0] ^ x[1] ^ x[2] ^ x[3];
+}
+
+__global__ void __launch_bounds__(512) mfma_f8_loop(int iters, float* __restrict__ sink) {
+  const int l = threadIdx.x & 63;
+  v8i a, b;
+  for (int i = 0; i < 8; ++i) {
+    a[i] = 0x38383838 ^ (l + i);  // e4m3 values near 1
+    b[i] = 0x38383838 ^ (3 * l + i);
+  }
+  v4f acc[kChains] = {};
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int j = 0; j < kChains; ++j)
+      acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[j], 0, 0, 0, 0, 0, 0);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kChains; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+__global__ void __launch_bounds__(512) mfma_bf16_loop(int iters, float* __restrict__ sink) {
+  const int l = threadIdx.x & 63;
+  v8bf a, b;
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (__bf16)(1.0f + (l + i) * 0.0078125f);
+    b[i] = (__bf16)(1.0f - (l + 2 * i) * 0.0039062f);
+  }
+  v4f acc[kChains] = {};
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int j = 0; j < kChains; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[j], 0, 0, 0);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kChains; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Reads `bytes` (a multiple of 16) of `src` once; `sink` holds blocks * 256
+// uint32.  Returns a hipError_t.
+int moe_bench_read_stream(const void* src, size_t bytes, void* sink, int blocks, hipStream_t stream) {
+  hipLaunchKernelGGL(read_stream, dim3(blocks), dim3(256), 0, stream, (const v4u*)src, bytes / 16, (uint32_t*)sink);
+  return (int)hipGetLastError();
+}
+
+// kind 0: fp8 f8f6f4 16x16x128, kind 1: bf16 16x16x32.  `blocks` workgroups
+// of 512 threads, each wave `iters` x 8 MFMAs; `sink` holds blocks * 512
+// floats.  FLOPs = blocks * 8 waves * iters * 8 * (2 * 16 * 16 * K).
+int moe_bench_mfma_loop(int kind, int iters, int blocks, void* sink, hipStream_t stream) {
+  if (kind == 0)
+    hipLaunchKernelGGL(mfma_f8_loop, dim3(blocks), dim3(512), 0, stream, iters, (float*)sink);
+  else
+    hipLaunchKernelGGL(mfma_bf16_loop, dim3(blocks), dim3(512), 0, stream, iters, (float*)sink);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"
