@@ -217,8 +217,7 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
       const float x2 = __shfl_xor(v, 8, kWave);
       const int r = 4 * lq + i;
       const int prow = kDirect ? (r < rows ? inv[r] : -1) : (r < rows ? row0 + rt * 16 + r : -1);
-      const float silu = x2 / (1.0f + expf(-x2));
-      split_bf16(silu * v, out.hi, out.lo);
+      split_bf16(silu_mul(x2, v), out.hi, out.lo);
       out.row = lr < 8 ? prow : -1;
     }
     lds_barrier();  // red / sa / inv consumed before they are rewritten
@@ -559,9 +558,8 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
         const int r = (wm * MI + mi) * 16 + 4 * lq + i;
         if (r < rows) {
           const float x1 = acc[mi][nj][i], x2 = acc[mi][nj + 2][i];
-          const float silu = x2 / (1.0f + expf(-x2));
           uint16_t hi, lo;
-          split_bf16(silu * x1, hi, lo);
+          split_bf16(silu_mul(x2, x1), hi, lo);
           uint16_t* p = act + (size_t)(row0 + r) * kActRowElems + act_col(j0 + 32 * wn + 16 * nj + lr);
           p[0] = hi;
           p[64] = lo;
@@ -811,9 +809,8 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float x1 = acc[mi][nj][i], x2 = acc[mi][C::NJ + nj][i];
-          const float silu = x2 / (1.0f + expf(-x2));
           uint16_t hi, lo;
-          split_bf16(silu * x1, hi, lo);
+          split_bf16(silu_mul(x2, x1), hi, lo);
           h[i] = hi;
           l[i] = lo;
         }

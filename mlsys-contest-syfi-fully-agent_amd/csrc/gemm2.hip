@@ -14,6 +14,8 @@
 // Two kernels: a streaming one for small T (weights read once into
 // registers, the routing-weighted combine fused in) and an LDS-tiled one for
 // large T (MFMA-bound; rows go to the combine pass as bf16).
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace moe {
@@ -432,10 +434,12 @@ hipError_t launch_gemm2_tiled(int T, const uint8_t* w2, const float* w2_scale, c
 //   * three 48 KB LDS stages, the copies of stages s+1 and s+2 in flight while
 //     stage s is multiplied; operand layouts as in the tiled path.
 // ---------------------------------------------------------------------------
-struct G2Wide {
-  static constexpr int kWaves = 8;
+template <int WAVES, int WM_, int WN_, int MI_>
+struct G2WideCfg {
+  static constexpr int kWaves = WAVES;
   static constexpr int kThreads = kWave * kWaves;
-  static constexpr int WM = 4, WN = 2, MI = 2, NJ = 8;
+  static constexpr int WM = WM_, WN = WN_, MI = MI_, NJ = 8;
+  static_assert(WM * WN == kWaves, "wave grid");
   static constexpr int BM = 16 * MI * WM;  // 128
   static constexpr int BN = 16 * NJ * WN;  // 256
   static constexpr int kNT = kH / BN;      // 28
@@ -450,18 +454,22 @@ struct G2Wide {
   static constexpr int kWscBytes = WN * kNIBlk * 4;
   static constexpr int kSteps = kI / 64;
   static constexpr int kPlanes = kAPlanes + kBFrags;
-  static constexpr int kPlanesPerWave = kPlanes / kWaves;  // 6: 4 A + 2 B
+  static constexpr int kPlanesPerWave = kPlanes / kWaves;
   static constexpr int kAPlanesPerWave = kAPlanes / kWaves;
   static constexpr int kGroupM = 4;
   static_assert(kPlanes % kWaves == 0 && kAPlanes % kWaves == 0, "planes split evenly");
   static_assert(kStages * kStageBytes + kWscBytes <= 160 * 1024, "LDS");
 };
+// 8 waves (2 per SIMD), wave tile 32 x 128
+using G2Wide = G2WideCfg<8, 4, 2, 2>;
 
-__global__ void __launch_bounds__(G2Wide::kThreads)
+// kPairScale: the weight scale is applied once per 128-K block (partials
+// kept across the block's two stages); otherwise once per 64-K stage.
+template <class C, bool kPairScale>
+__global__ void __launch_bounds__(C::kThreads)
 gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
                   const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
                   float* __restrict__ down) {
-  using C = G2Wide;
   __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
 
   ExpertRows X;
@@ -509,20 +517,16 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
       dst[k] = C::kBOff + f * 1024;
     }
   }
+  // Every wave issues all its planes at every stage, so the number of copies
+  // in flight per stage is a compile-time constant (the A rows of a partial
+  // tile's last fragments repeat the tile's last row; they are never read).
   auto issue = [&](int s) {
     char* base = lds + (s % C::kStages) * C::kStageBytes;
     const char* ak = actb + s * 256;
     const uint8_t* wk = w2e + s * 64;
 #pragma unroll
-    for (int k = 0; k < C::kPlanesPerWave; ++k) {
-      const bool a_plane = k < C::kAPlanesPerWave;
-      // A fragments wholly past the tile's rows are never read: no copy
-      if (a_plane) {
-        if (((wave + k * C::kWaves) >> 2) * 16 < rows) dma16(ak + off[k], base + dst[k]);
-      } else {
-        dma16(wk + off[k], base + dst[k]);
-      }
-    }
+    for (int k = 0; k < C::kPlanesPerWave; ++k)
+      dma16(k < C::kAPlanesPerWave ? (const void*)(ak + off[k]) : (const void*)(wk + off[k]), base + dst[k]);
   };
   float* wsc = (float*)(lds + C::kStages * C::kStageBytes);  // [WN][16]
   for (int i = threadIdx.x; i < C::WN * kNIBlk; i += C::kThreads) {
@@ -530,13 +534,20 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
     wsc[i] = w2_scale[((size_t)e * kNHBlk + (n0 + 16 * C::NJ * w_n) / kBlk) * kNIBlk + kb];
   }
 
-  v4f acc[C::MI][C::NJ];
+  v4f acc[C::MI][C::NJ], P[C::MI][C::NJ];
 #pragma unroll
   for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
-    for (int nj = 0; nj < C::NJ; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int nj = 0; nj < C::NJ; ++nj) acc[mi][nj] = P[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int s) {
+  // One 64-K stage.  A 128-K weight scale block spans an even stage and the
+  // odd stage after it: P[mi][nj] collects the block's partial products over
+  // both (MFMA accumulation), and only the odd stage applies the scale,
+  // acc += P * w_scale, once per block.
+  auto compute = [&](int s, auto odd_c) {
+    // kApply: this stage applies the scale; kCont: it continues the block's partials
+    constexpr bool kApply = !kPairScale || decltype(odd_c)::value;
+    constexpr bool kCont = kPairScale && decltype(odd_c)::value;
     const char* sbuf = lds + (s % C::kStages) * C::kStageBytes;
     auto bread = [&](int nj) { return *(const v4i*)(sbuf + C::kBOff + (wn * C::NJ + nj) * 1024 + slot_b); };
     // LDS reads in the order of first use, B fragments two blocks ahead: the
@@ -553,65 +564,73 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
       al[mi][1] = *(const v8bf*)(f + 2048 + slot_a1);
     }
     braw[1] = bread(1);
-    const float sb = wsc[wn * kNIBlk + (s >> 1)];
-    // Software-pipelined over column blocks: the scale FMAs of block nj - 1
-    // are issued after the MFMAs of block nj, so the VALU work runs while the
-    // matrix core is busy; each block's MFMA results live for one block.
-    v4f pp[C::MI];
+    const float sb = kApply ? wsc[wn * kNIBlk + (s >> 1)] : 0.f;
+    // W2 fragments widened to bf16 one column block ahead, into the other of
+    // two register sets: block nj's MFMAs never wait for their conversion,
+    // and no conversion overwrites registers an issued MFMA still reads.
+    v8bf bc[2][2];
+    bc[0][0] = e4m3x8_to_bf16((uint32_t)braw[0][0], (uint32_t)braw[0][1]);
+    bc[0][1] = e4m3x8_to_bf16((uint32_t)braw[0][2], (uint32_t)braw[0][3]);
 #pragma unroll
     for (int nj = 0; nj < C::NJ; ++nj) {
       if (nj + 2 < C::NJ) braw[nj + 2] = bread(nj + 2);
-      const v4i raw = braw[nj];
-      const v8bf b0 = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
-      const v8bf b1 = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
+      const v8bf b0 = bc[nj & 1][0], b1 = bc[nj & 1][1];
       // operands swapped (W2 rows as the MFMA's A): lane (q, r) receives
       // row r, columns 4q .. 4q+3 of the block, stored as one 16-byte write
-      v4f pc[C::MI];
 #pragma unroll
       for (int mi = 0; mi < C::MI; ++mi) {
-        pc[mi] = mfma_bf16_16x16x32(b0, a[mi][0], v4f{0.f, 0.f, 0.f, 0.f});
-        pc[mi] = mfma_bf16_16x16x32(b1, a[mi][1], pc[mi]);
-        pc[mi] = mfma_bf16_16x16x32(b0, al[mi][0], pc[mi]);
-        pc[mi] = mfma_bf16_16x16x32(b1, al[mi][1], pc[mi]);
+        v4f p = kCont ? P[mi][nj] : v4f{0.f, 0.f, 0.f, 0.f};
+        p = mfma_bf16_16x16x32(b0, a[mi][0], p);
+        p = mfma_bf16_16x16x32(b1, a[mi][1], p);
+        p = mfma_bf16_16x16x32(b0, al[mi][0], p);
+        p = mfma_bf16_16x16x32(b1, al[mi][1], p);
+        P[mi][nj] = p;
       }
-      if (nj > 0) {
+      if (nj + 1 < C::NJ) {
+        const v4i raw = braw[nj + 1];
+        bc[(nj + 1) & 1][0] = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
+        bc[(nj + 1) & 1][1] = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
+      }
+      // the scale FMAs of block nj - 1, whose MFMAs have finished, run
+      // while the matrix core works on block nj
+      if (kApply && nj > 0) {
 #pragma unroll
         for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[mi][nj - 1][i] = __builtin_fmaf(pp[mi][i], sb, acc[mi][nj - 1][i]);
+          for (int i = 0; i < 4; ++i) acc[mi][nj - 1][i] = __builtin_fmaf(P[mi][nj - 1][i], sb, acc[mi][nj - 1][i]);
       }
-#pragma unroll
-      for (int mi = 0; mi < C::MI; ++mi) pp[mi] = pc[mi];
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (kApply) {
 #pragma unroll
-    for (int mi = 0; mi < C::MI; ++mi)
+      for (int mi = 0; mi < C::MI; ++mi)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[mi][C::NJ - 1][i] = __builtin_fmaf(pp[mi][i], sb, acc[mi][C::NJ - 1][i]);
+        for (int i = 0; i < 4; ++i) acc[mi][C::NJ - 1][i] = __builtin_fmaf(P[mi][C::NJ - 1][i], sb, acc[mi][C::NJ - 1][i]);
+    }
   };
 
-  // Waves whose 64 rows all lie past the tile's rows only help with copies.
+  // Waves whose rows all lie past the tile's rows only help with copies.
   const bool wave_live = C::MI * 16 * wm < rows;
-  // copies this wave issues per stage (the same for every stage)
-  int ops_per_stage = 0;
-#pragma unroll
-  for (int k = 0; k < C::kPlanesPerWave; ++k)
-    ops_per_stage += (k >= C::kAPlanesPerWave || ((wave + k * C::kWaves) >> 2) * 16 < rows) ? 1 : 0;
-
+  // Step s: stage s has landed (stage s + 1 may stay in flight) and every wave
+  // has finished reading stage s - 1, whose buffer takes stage s + 2 after the
+  // barrier.
+  auto step = [&](int s, auto odd_c) {
+    if (s + 1 < C::kSteps)
+      wait_vmcnt_lgkm0<C::kPlanesPerWave>();
+    else
+      wait_vmcnt_lgkm0<0>();
+    block_barrier();
+    if (s + C::kStages - 1 < C::kSteps) issue(s + C::kStages - 1);
+    if (wave_live) compute(s, odd_c);
+  };
+  static_assert(C::kSteps % 2 == 0 && C::kStages == 3, "stage pairs; one stage in flight at each wait");
 #pragma unroll
   for (int s = 0; s < C::kStages - 1; ++s) issue(s);
 #pragma unroll 1
-  for (int s = 0; s < C::kSteps - 1; ++s) {
-    // stage s landed (stage s+1 may stay in flight); every wave has finished
-    // reading stage s-1, whose buffer takes stage s+2 after the barrier
-    wait_vmcnt_lgkm0_rt(ops_per_stage);
-    block_barrier();
-    if (s + C::kStages - 1 < C::kSteps) issue(s + C::kStages - 1);
-    if (wave_live) compute(s);
+  for (int s = 0; s < C::kSteps; s += 2) {
+    step(s, std::false_type{});
+    step(s + 1, std::true_type{});
   }
-  wait_vmcnt_lgkm0<0>();
-  block_barrier();
-  if (wave_live) compute(C::kSteps - 1);
 
 #pragma unroll
   for (int mi = 0; mi < C::MI; ++mi) {
@@ -624,13 +643,13 @@ gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ 
   }
 }
 
+template <class C, bool kPairScale>
 hipError_t launch_gemm2_wide(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
                              hipStream_t stream) {
-  using C = G2Wide;
   const int64_t pairs = (int64_t)T * kTopK;
   const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
   const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
-  hipLaunchKernelGGL(gemm2_wide_kernel, dim3((unsigned)blocks), dim3(C::kThreads), 0, stream,
+  hipLaunchKernelGGL((gemm2_wide_kernel<C, kPairScale>), dim3((unsigned)blocks), dim3(C::kThreads), 0, stream,
                      (const uint16_t*)(ws + L.act), w2, w2_scale, (const int32_t*)(ws + L.expert_off),
                      (float*)(ws + L.down));
   return hipGetLastError();
@@ -649,7 +668,7 @@ hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const L
     return hipGetLastError();
   }
   if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<2, 4, 2, 4, 3>(T, w2, w2_scale, L, ws, stream);
-  return launch_gemm2_wide(T, w2, w2_scale, L, ws, stream);
+  return launch_gemm2_wide<G2Wide, true>(T, w2, w2_scale, L, ws, stream);
 }
 
 }  // namespace moe

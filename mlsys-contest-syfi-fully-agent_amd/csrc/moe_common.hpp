@@ -144,6 +144,17 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) 
   lo = __builtin_isfinite(h) ? f32_to_bf16_rne(v - h) : (uint16_t)0;
 }
 
+// SwiGLU of one (gate x1, up x2) pair: silu(x2) * x1 = x2 / (1 + e^-x2) * x1
+// (moe.py:190-193), with the hardware exp2 and reciprocal (v_exp_f32,
+// v_rcp_f32: ~1 ulp each) in place of correctly rounded division: a few ulp
+// against the reference's fp32 ops, far below the ~1e-5 relative error the
+// fp8 MFMA block sums already carry into x1 and x2.  x2 -> -inf gives -0 as
+// the reference does (e^-x2 = inf, rcp = 0).
+__device__ __forceinline__ float silu_mul(float x2, float x1) {
+  const float e = __builtin_amdgcn_exp2f(-x2 * 1.44269504088896341f);
+  return x2 * __builtin_amdgcn_rcpf(1.0f + e) * x1;
+}
+
 // Order-preserving map of a (non-NaN) float to uint32.
 __device__ __forceinline__ uint32_t float_order_key(float v) {
   uint32_t u = __float_as_uint(v);
