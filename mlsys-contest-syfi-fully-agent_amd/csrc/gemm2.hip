@@ -5,17 +5,17 @@
 // solution gemm_fp32_fp8w_fused_acc_grouped_kernel (moe.cu:2186-2431), which
 // emulates fp32 A with hi/lo bf16 pairs.
 //
-// Precision choice: the activation C is kept in bf16 (relative rounding 2^-9,
-// ~0.1% of the output scale after the 2048-term sum) and the e4m3 weights are
-// widened exactly to bf16, so GEMM2 runs on v_mfma_f32_16x16x32_bf16.  A single
-// e4m3 rounding of C (2^-4 relative) would break the 1e-2 tolerance; a hi/lo
-// e4m3 split costs the same MFMA time as bf16.
+// Precision: the activation C arrives as a bf16 (hi, lo) pair (hi + lo
+// carries the fp32 SwiGLU value to ~2^-17) and the e4m3 weights are widened
+// exactly to bf16, so every product of the fp32 reference is formed: two
+// v_mfma_f32_16x16x32_bf16 per operand pair, fp32 accumulation (this MFMA
+// sums to fp32 accuracy; the fp8 one does not -- see gemm1.hip).  That is the
+// reference CUDA's own hi/lo design; a single bf16 C fails the 1e-2 check on
+// several percent of the elements once outputs reach ~1e3.
 //
-// Two kernels: a streaming one for small T (weights read once into
-// registers, the routing-weighted combine fused in) and an LDS-tiled one for
-// large T (MFMA-bound; rows go to the combine pass as bf16).
-#include <type_traits>
-
+// Two kernels: a streaming one for T <= 64 (weights read once, the
+// routing-weighted combine fused in) and an LDS-tiled one for larger T (fp32
+// rows to the combine pass).
 #include "kernels.hpp"
 
 namespace moe {
@@ -239,15 +239,18 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
 //     with scale 1); P accumulates the two stages of a 128-K scale block on
 //     v_mfma_f32_16x16x32_bf16, then acc += P * w_scale[n/128, kb].
 // ---------------------------------------------------------------------------
-// Token count from which GEMM2 uses the wide 256 x 256 tiles.  Below it,
-// 64 x 256 tiles of 8 waves with a 3-stage ring: at T = 1024 they ran 95 us
-// against 104 us for 64 x 128 tiles with 4 stages.  The wider tile copies each
-// activation row once per 256 weight rows instead of once per 128, and at
-// 72 KB of LDS two workgroups still fit on a CU.  They also beat the wide
-// tiles up to T = 4096 (T = 2048: 138 against 195-211 us); where they lose
-// depends on the rows per active expert, which the host does not know: with
-// four hot experts they tie at T = 4096 and trail by 2.5% at T = 6144.
-constexpr int kGemm2TiledLargeMinTokens = 4096;
+// One tile shape serves every T > 64: 64 rows x 256 columns, 8 waves, two
+// 32 KB stages, so two workgroups (16 waves) share a CU.  Each stage holds
+// 64 K of the rows' bf16 hi and lo halves (128 + 128 bytes per row) and of
+// 256 W2 rows.  With the activation pair, a three-stage ring (96 KB) would
+// leave one workgroup per CU; measured against it and against 128 x 256
+// tiles of 8 waves with three 48 KB stages (one per CU), the two-workgroup
+// form was fastest at every T tried: T = 1024 113 against 140 us, T = 4000
+// 830 against 1030 us, T = 8192 with four hot experts 1677 against 1816 us
+// (the 128 x 256 kernel), uniform routing at T = 8192 537 against 612 us.
+// Sixteen resident waves hide the stage barrier and the operand reads that
+// eight could not: with eight, the first wave of each SIMD finishes its
+// stage early and waits at the barrier while the second runs alone.
 
 template <int WM, int WN, int MI, int NJ, int STAGES>
 struct G2Tiled {
@@ -419,242 +422,6 @@ hipError_t launch_gemm2_tiled(int T, const uint8_t* w2, const float* w2_scale, c
   return hipGetLastError();
 }
 
-// ---------------------------------------------------------------------------
-// Wide path (large T): 128 rows x 256 columns per workgroup.  Each row carries
-// its activation as a hi and a lo bf16 plane, so a 64-K stage holds
-// 128 x 256 B of activation and 256 x 64 B of W2 (48 KB), and multiplying it
-// takes as many MFMAs as a 256 x 256 tile of single bf16 rows.  The L2 -> LDS
-// copy rate per CU, not the MFMAs, bounds narrower tiles.
-//
-//   * 8 waves as 4 (rows) x 2 (columns); wave tile 32 rows x 128 columns (one
-//     128-column weight scale block), 2 x 8 MFMA blocks of four MFMAs each
-//     (hi and lo, two 32-K halves), 64 accumulator VGPRs;
-//   * the scale is applied per 64-K stage (acc += P_stage * w_scale[n/128,
-//     k/128]), so no second set of block partials stays live across stages;
-//   * three 48 KB LDS stages, the copies of stages s+1 and s+2 in flight while
-//     stage s is multiplied; operand layouts as in the tiled path.
-// ---------------------------------------------------------------------------
-template <int WAVES, int WM_, int WN_, int MI_>
-struct G2WideCfg {
-  static constexpr int kWaves = WAVES;
-  static constexpr int kThreads = kWave * kWaves;
-  static constexpr int WM = WM_, WN = WN_, MI = MI_, NJ = 8;
-  static_assert(WM * WN == kWaves, "wave grid");
-  static constexpr int BM = 16 * MI * WM;  // 128
-  static constexpr int BN = 16 * NJ * WN;  // 256
-  static constexpr int kNT = kH / BN;      // 28
-  static_assert(kH % BN == 0 && 16 * NJ == kBlk, "a wave's columns are one scale block");
-  static constexpr int kAFrags = BM / 16;
-  static constexpr int kAFragBytes = 4096;  // hi (two wide planes), then lo (two wide planes)
-  static constexpr int kAPlanes = 4 * kAFrags;
-  static constexpr int kBFrags = BN / 16;
-  static constexpr int kBOff = kAFrags * kAFragBytes;
-  static constexpr int kStageBytes = kBOff + kBFrags * 1024;  // 48 KB
-  static constexpr int kStages = 3;
-  static constexpr int kWscBytes = WN * kNIBlk * 4;
-  static constexpr int kSteps = kI / 64;
-  static constexpr int kPlanes = kAPlanes + kBFrags;
-  static constexpr int kPlanesPerWave = kPlanes / kWaves;
-  static constexpr int kAPlanesPerWave = kAPlanes / kWaves;
-  static constexpr int kGroupM = 4;
-  static_assert(kPlanes % kWaves == 0 && kAPlanes % kWaves == 0, "planes split evenly");
-  static_assert(kStages * kStageBytes + kWscBytes <= 160 * 1024, "LDS");
-};
-// 8 waves (2 per SIMD), wave tile 32 x 128
-using G2Wide = G2WideCfg<8, 4, 2, 2>;
-
-// kPairScale: the weight scale is applied once per 128-K block (partials
-// kept across the block's two stages); otherwise once per 64-K stage.
-template <class C, bool kPairScale>
-__global__ void __launch_bounds__(C::kThreads)
-gemm2_wide_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
-                  const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
-                  float* __restrict__ down) {
-  __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
-
-  ExpertRows X;
-  X.load(expert_off);
-  const int mt_total = X.count_tiles(C::BM);
-  const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
-  if (t < 0) return;
-  int mt, nt;
-  grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
-  int e, row0, rows;
-  X.find_tile(mt, C::BM, e, row0, rows);
-  const int n0 = nt * C::BN;
-
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int lane = threadIdx.x & (kWave - 1);
-  const int lq = lane >> 4;
-  const int lr = lane & 15;
-  const int wm = wave / C::WN;
-  const int wn = wave % C::WN;
-  // MFMA operand slots: A rows in wide layout (chunks 2q, 2q+1), B rows narrow (chunk q)
-  const int slot_a0 = wide_slot(lr, 2 * lq), slot_a1 = wide_slot(lr, 2 * lq + 1), slot_b = narrow_slot(lr, lq);
-
-  // DMA planes wave + 8k: k < 4 are A planes (act rows), k >= 4 B planes.
-  // A plane 4f + 2h + p: rows 8p .. 8p+7 of row block f, hi (h = 0) or lo
-  // (h = 1) half of the stage's 64 columns (adjacent 128-byte runs of the row).
-  const char* actb = (const char*)(act + (size_t)row0 * kActRowElems);
-  const uint8_t* w2e = w2 + (size_t)e * kH * kI;
-  uint32_t off[C::kPlanesPerWave];
-  int dst[C::kPlanesPerWave];
-#pragma unroll
-  for (int k = 0; k < C::kPlanesPerWave; ++k) {
-    const int plane = wave + k * C::kWaves;
-    if (plane < C::kAPlanes) {
-      const int f = plane >> 2, h = (plane >> 1) & 1, p = plane & 1;
-      int fr, chunk;
-      wide_copy_lane(lane, p, fr, chunk);
-      const int r = min(f * 16 + fr, rows - 1);
-      off[k] = (uint32_t)(r * kActRowElems * 2 + 128 * h + 16 * chunk);
-      dst[k] = f * C::kAFragBytes + h * 2048 + p * 1024;
-    } else {
-      const int f = plane - C::kAPlanes;
-      int fr, chunk;
-      narrow_copy_lane(lane, fr, chunk);
-      off[k] = (uint32_t)(n0 + 16 * f + fr) * kI + 16 * chunk;
-      dst[k] = C::kBOff + f * 1024;
-    }
-  }
-  // Every wave issues all its planes at every stage, so the number of copies
-  // in flight per stage is a compile-time constant (the A rows of a partial
-  // tile's last fragments repeat the tile's last row; they are never read).
-  auto issue = [&](int s) {
-    char* base = lds + (s % C::kStages) * C::kStageBytes;
-    const char* ak = actb + s * 256;
-    const uint8_t* wk = w2e + s * 64;
-#pragma unroll
-    for (int k = 0; k < C::kPlanesPerWave; ++k)
-      dma16(k < C::kAPlanesPerWave ? (const void*)(ak + off[k]) : (const void*)(wk + off[k]), base + dst[k]);
-  };
-  float* wsc = (float*)(lds + C::kStages * C::kStageBytes);  // [WN][16]
-  for (int i = threadIdx.x; i < C::WN * kNIBlk; i += C::kThreads) {
-    const int w_n = i / kNIBlk, kb = i % kNIBlk;
-    wsc[i] = w2_scale[((size_t)e * kNHBlk + (n0 + 16 * C::NJ * w_n) / kBlk) * kNIBlk + kb];
-  }
-
-  v4f acc[C::MI][C::NJ], P[C::MI][C::NJ];
-#pragma unroll
-  for (int mi = 0; mi < C::MI; ++mi)
-#pragma unroll
-    for (int nj = 0; nj < C::NJ; ++nj) acc[mi][nj] = P[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // One 64-K stage.  A 128-K weight scale block spans an even stage and the
-  // odd stage after it: P[mi][nj] collects the block's partial products over
-  // both (MFMA accumulation), and only the odd stage applies the scale,
-  // acc += P * w_scale, once per block.
-  auto compute = [&](int s, auto odd_c) {
-    // kApply: this stage applies the scale; kCont: it continues the block's partials
-    constexpr bool kApply = !kPairScale || decltype(odd_c)::value;
-    constexpr bool kCont = kPairScale && decltype(odd_c)::value;
-    const char* sbuf = lds + (s % C::kStages) * C::kStageBytes;
-    auto bread = [&](int nj) { return *(const v4i*)(sbuf + C::kBOff + (wn * C::NJ + nj) * 1024 + slot_b); };
-    // LDS reads in the order of first use, B fragments two blocks ahead: the
-    // first MFMAs wait only for their own operands
-    v4i braw[C::NJ];
-    braw[0] = bread(0);
-    v8bf a[C::MI][2], al[C::MI][2];
-#pragma unroll
-    for (int mi = 0; mi < C::MI; ++mi) {
-      const char* f = sbuf + (wm * C::MI + mi) * C::kAFragBytes;
-      a[mi][0] = *(const v8bf*)(f + slot_a0);
-      a[mi][1] = *(const v8bf*)(f + slot_a1);
-      al[mi][0] = *(const v8bf*)(f + 2048 + slot_a0);
-      al[mi][1] = *(const v8bf*)(f + 2048 + slot_a1);
-    }
-    braw[1] = bread(1);
-    const float sb = kApply ? wsc[wn * kNIBlk + (s >> 1)] : 0.f;
-    // W2 fragments widened to bf16 one column block ahead, into the other of
-    // two register sets: block nj's MFMAs never wait for their conversion,
-    // and no conversion overwrites registers an issued MFMA still reads.
-    v8bf bc[2][2];
-    bc[0][0] = e4m3x8_to_bf16((uint32_t)braw[0][0], (uint32_t)braw[0][1]);
-    bc[0][1] = e4m3x8_to_bf16((uint32_t)braw[0][2], (uint32_t)braw[0][3]);
-#pragma unroll
-    for (int nj = 0; nj < C::NJ; ++nj) {
-      if (nj + 2 < C::NJ) braw[nj + 2] = bread(nj + 2);
-      const v8bf b0 = bc[nj & 1][0], b1 = bc[nj & 1][1];
-      // operands swapped (W2 rows as the MFMA's A): lane (q, r) receives
-      // row r, columns 4q .. 4q+3 of the block, stored as one 16-byte write
-#pragma unroll
-      for (int mi = 0; mi < C::MI; ++mi) {
-        v4f p = kCont ? P[mi][nj] : v4f{0.f, 0.f, 0.f, 0.f};
-        p = mfma_bf16_16x16x32(b0, a[mi][0], p);
-        p = mfma_bf16_16x16x32(b1, a[mi][1], p);
-        p = mfma_bf16_16x16x32(b0, al[mi][0], p);
-        p = mfma_bf16_16x16x32(b1, al[mi][1], p);
-        P[mi][nj] = p;
-      }
-      if (nj + 1 < C::NJ) {
-        const v4i raw = braw[nj + 1];
-        bc[(nj + 1) & 1][0] = e4m3x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
-        bc[(nj + 1) & 1][1] = e4m3x8_to_bf16((uint32_t)raw[2], (uint32_t)raw[3]);
-      }
-      // the scale FMAs of block nj - 1, whose MFMAs have finished, run
-      // while the matrix core works on block nj
-      if (kApply && nj > 0) {
-#pragma unroll
-        for (int mi = 0; mi < C::MI; ++mi)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[mi][nj - 1][i] = __builtin_fmaf(P[mi][nj - 1][i], sb, acc[mi][nj - 1][i]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (kApply) {
-#pragma unroll
-      for (int mi = 0; mi < C::MI; ++mi)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mi][C::NJ - 1][i] = __builtin_fmaf(P[mi][C::NJ - 1][i], sb, acc[mi][C::NJ - 1][i]);
-    }
-  };
-
-  // Waves whose rows all lie past the tile's rows only help with copies.
-  const bool wave_live = C::MI * 16 * wm < rows;
-  // Step s: stage s has landed (stage s + 1 may stay in flight) and every wave
-  // has finished reading stage s - 1, whose buffer takes stage s + 2 after the
-  // barrier.
-  auto step = [&](int s, auto odd_c) {
-    if (s + 1 < C::kSteps)
-      wait_vmcnt_lgkm0<C::kPlanesPerWave>();
-    else
-      wait_vmcnt_lgkm0<0>();
-    block_barrier();
-    if (s + C::kStages - 1 < C::kSteps) issue(s + C::kStages - 1);
-    if (wave_live) compute(s, odd_c);
-  };
-  static_assert(C::kSteps % 2 == 0 && C::kStages == 3, "stage pairs; one stage in flight at each wait");
-#pragma unroll
-  for (int s = 0; s < C::kStages - 1; ++s) issue(s);
-#pragma unroll 1
-  for (int s = 0; s < C::kSteps; s += 2) {
-    step(s, std::false_type{});
-    step(s + 1, std::true_type{});
-  }
-
-#pragma unroll
-  for (int mi = 0; mi < C::MI; ++mi) {
-    const int r = (wm * C::MI + mi) * 16 + lr;
-    if (r < rows) {
-      float* drow = down + (size_t)(row0 + r) * kH + n0 + 16 * wn * C::NJ + 4 * lq;
-#pragma unroll
-      for (int nj = 0; nj < C::NJ; ++nj) *(v4f*)(drow + 16 * nj) = acc[mi][nj];
-    }
-  }
-}
-
-template <class C, bool kPairScale>
-hipError_t launch_gemm2_wide(int T, const uint8_t* w2, const float* w2_scale, const Layout& L, char* ws,
-                             hipStream_t stream) {
-  const int64_t pairs = (int64_t)T * kTopK;
-  const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
-  const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
-  hipLaunchKernelGGL((gemm2_wide_kernel<C, kPairScale>), dim3((unsigned)blocks), dim3(C::kThreads), 0, stream,
-                     (const uint16_t*)(ws + L.act), w2, w2_scale, (const int32_t*)(ws + L.expert_off),
-                     (float*)(ws + L.down));
-  return hipGetLastError();
-}
-
 }  // namespace
 
 bool gemm2_fuses_combine(int T) { return T <= kGemm2StreamMaxTokens; }
@@ -667,8 +434,7 @@ hipError_t launch_gemm2(int T, const uint8_t* w2, const float* w2_scale, const L
                        (const int32_t*)(ws + L.perm_token), (const float*)(ws + L.perm_w), T, (uint16_t*)out);
     return hipGetLastError();
   }
-  if (T < kGemm2TiledLargeMinTokens) return launch_gemm2_tiled<2, 4, 2, 4, 3>(T, w2, w2_scale, L, ws, stream);
-  return launch_gemm2_wide<G2Wide, true>(T, w2, w2_scale, L, ws, stream);
+  return launch_gemm2_tiled<2, 4, 2, 4, 2>(T, w2, w2_scale, L, ws, stream);
 }
 
 }  // namespace moe

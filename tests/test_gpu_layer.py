@@ -51,8 +51,8 @@ LAYER_CASES = [
     ("skewed_t8192", None, 1025, None),   # smallest T of the wide GEMM1
     ("skewed_t8192", None, 2047, None),
     ("skewed_t8192", None, 2048, None),
-    ("skewed_t8192", None, 4095, None),   # largest T of the tiled GEMM2
-    ("skewed_t8192", None, 4096, None),   # smallest T of the wide GEMM2
+    ("skewed_t8192", None, 4095, None),
+    ("skewed_t8192", None, 4096, None),
     # the contest dataset's largest T (moe.py:13), sampled
     ("skewed_t8192", None, 14107, 768),
 ]
@@ -114,7 +114,7 @@ def test_layer_matches_reference_golden(pkg, cuda_device, name):
 INTERMEDIATE_CASES = [
     ("small_t64", None, None),          # row-streaming kernels
     ("prefill_t1024", None, 200),
-    ("skewed_t8192", 2304, 160),        # LDS-tiled kernels, ragged last tiles
+    ("skewed_t8192", 2304, 160),        # LDS-tiled / wide kernels, ragged last tiles
 ]
 
 
