@@ -805,18 +805,15 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
       const int c0 = j0 + 16 * C::NJ * wn + 4 * lq;  // 4 adjacent columns: one 8-byte store per half
 #pragma unroll
       for (int nj = 0; nj < C::NJ; ++nj) {
-        uint32_t h[4], l[4];
+        float c[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float x1 = acc[mi][nj][i], x2 = acc[mi][C::NJ + nj][i];
-          uint16_t hi, lo;
-          split_bf16(silu_mul(x2, x1), hi, lo);
-          h[i] = hi;
-          l[i] = lo;
-        }
+        for (int i = 0; i < 4; ++i) c[i] = silu_mul(acc[mi][C::NJ + nj][i], acc[mi][nj][i]);
+        uint2 h, l;
+        split_bf16x2(c[0], c[1], h.x, l.x);
+        split_bf16x2(c[2], c[3], h.y, l.y);
         uint16_t* p = arow + act_col(c0 + 16 * nj);
-        *(uint2*)p = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-        *(uint2*)(p + 64) = uint2{l[0] | (l[1] << 16), l[2] | (l[3] << 16)};
+        *(uint2*)p = h;
+        *(uint2*)(p + 64) = l;
       }
     }
   }

@@ -136,12 +136,31 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
-// v -> (hi, lo) bf16 bits with hi = RNE(v), lo = RNE(v - hi); v - hi is exact
-// in fp32.  Non-finite hi keeps lo = 0, so hi + lo stays inf / NaN like v.
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+
+// (a, b) -> bf16 bits a | b << 16, both rounded to nearest even, in one
+// v_cvt_pk_bf16_f32 (equal to f32_to_bf16_rne for every fp32 but NaN payloads;
+// checked exhaustively by the test suite).
+__device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{a, b}, v2bf_t));
+}
+
+// Two values -> their (hi, lo) bf16 pairs, packed as bf16x2_rne packs:
+// hi = RNE(v), lo = RNE(v - hi); v - hi is exact in fp32.  A non-finite hi
+// keeps lo = 0, so hi + lo stays inf / NaN like v.
+__device__ __forceinline__ void split_bf16x2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = bf16x2_rne(a, b);
+  const float ha = __uint_as_float(hi << 16), hb = __uint_as_float(hi & 0xFFFF0000u);
+  lo = bf16x2_rne(__builtin_isfinite(ha) ? a - ha : 0.f, __builtin_isfinite(hb) ? b - hb : 0.f);
+}
+
+// One value -> its (hi, lo) bf16 pair.
 __device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
-  hi = f32_to_bf16_rne(v);
-  const float h = bf16_to_f32(hi);
-  lo = __builtin_isfinite(h) ? f32_to_bf16_rne(v - h) : (uint16_t)0;
+  uint32_t h, l;
+  split_bf16x2(v, 0.f, h, l);
+  hi = (uint16_t)h;
+  lo = (uint16_t)l;
 }
 
 // SwiGLU of one (gate x1, up x2) pair: silu(x2) * x1 = x2 / (1 + e^-x2) * x1

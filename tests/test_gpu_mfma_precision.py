@@ -83,3 +83,16 @@ def test_bf16_chain_is_fp32_accurate(cuda_device):
         e = _rel_err(D, exact, absum)
         print(f"  err / sum|p|: max 2^{np.log2(e.max()):.1f}, rms 2^{np.log2(np.sqrt((e ** 2).mean())):.1f}")
         assert e.max() < 2.0 ** -20      # fp32 accumulation
+
+
+def test_bf16_convert_instruction_exhaustive(cuda_device):
+    """v_cvt_pk_bf16_f32, which the SwiGLU epilogues use to split each fp32
+    activation into its bf16 (hi, lo) pair, rounds every finite and infinite
+    fp32 exactly like software round-to-nearest-even, keeps NaN a NaN, and
+    puts element 0 in the low half (tests/support/cvt_check.hip)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "support", "_build", "libcvt_check.so")
+    L = ctypes.CDLL(path)
+    counts = (ctypes.c_ulonglong * 3)()
+    print("bf16_check: 2^32 fp32 patterns", flush=True)
+    assert L.bf16_check(counts) == 0
+    assert list(counts) == [0, 0, 0], list(counts)
