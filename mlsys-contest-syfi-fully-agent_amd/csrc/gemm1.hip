@@ -370,7 +370,7 @@ struct G1Tiled {
 };
 
 template <int WM, int WN, int MI>
-__global__ void __launch_bounds__(64 * WM * WN)
+__global__ void __launch_bounds__(64 * WM * WN, 4)
 gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
                    const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                    const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
@@ -453,11 +453,10 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // Software pipeline.  At iteration kb the operands of stage kb are already
-  // in registers (read during iteration kb - 1), so
-  //   * its LDS buffer takes the DMA of stage kb + kStages at once (the DMA
-  //     stays kStages - 1 stages ahead of the LDS reads), and
-  //   * the LDS reads of stage kb + 1 overlap the MFMAs of stage kb.
+  // Pipeline: the DMA of a stage is issued kStages - 1 steps before its
+  // operands are read, and the kernel is capped at 128 VGPRs (launch bounds
+  // of 4 waves per SIMD) so that two workgroups share a CU; the LDS reads of
+  // one workgroup overlap the MFMAs of the other.
   struct Frags {
     v8i a[MI], b[4];
     v4f sa[MI];
@@ -501,52 +500,23 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
     for (int mi = 0; mi < MI; ++mi) compute_row(F, mi);
   };
 
-  // One pipeline step: stage kb+1 has landed (later stages may stay in
-  // flight) and this wave's reads of stage kb are complete (the wait also
-  // drains LDS reads), so after the barrier stage kb's buffer is free.
-  // The A fragment of row block mi of stage kb+1 is read once the MFMAs of
-  // row block mi of stage kb have taken theirs, so both stages' A fragments
-  // are never live at once.
-  auto step = [&](int kb, const Frags& c, Frags& n, int ahead, bool refill) {
-    wait_stages_ahead<C::kDmaPerStage>(ahead);
-    block_barrier();
-    if (refill) issue(kb + C::kStages);
-    read_b(kb + 1, n);
+  // One fragment set, read at the start of each step: with four waves per
+  // SIMD the other waves cover the LDS latency.  Step kb: stage kb has
+  // landed (later stages may stay in flight) and, after the barrier, every
+  // wave is done with stage kb - 1, whose buffer takes stage kb + kStages - 1.
+  Frags f;
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-      compute_row(c, mi);
-      __builtin_amdgcn_sched_barrier(0);
-      read_a(kb + 1, mi, n);
-    }
-  };
-  // Two fragment sets used alternately (no register copies between steps);
-  // every branch below is resolved at compile time, so the compiler sees
-  // straight-line code between the explicit waits.
-  constexpr int kRefill = kNHBlk - C::kStages;  // steps that refill their buffer
-  constexpr int kPairs = kRefill / 2;
-  Frags f0, f1;
-#pragma unroll
-  for (int s = 0; s < C::kStages; ++s) issue(s);
-  wait_stages_ahead<C::kDmaPerStage>(C::kStages - 1);  // stage 0 landed
-  block_barrier();
-  read_b(0, f0);
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi) read_a(0, mi, f0);
+  for (int s = 0; s < C::kStages - 1; ++s) issue(s);
 #pragma unroll 1
-  for (int p = 0; p < kPairs; ++p) {
-    step(2 * p, f0, f1, C::kStages - 2, true);
-    step(2 * p + 1, f1, f0, C::kStages - 2, true);
-  }
+  for (int kb = 0; kb < kNHBlk; ++kb) {
+    wait_stages_ahead<C::kDmaPerStage>(min(C::kStages - 2, kNHBlk - 1 - kb));
+    block_barrier();
+    if (kb + C::kStages - 1 < kNHBlk) issue(kb + C::kStages - 1);
+    read_b(kb, f);
 #pragma unroll
-  for (int kb = 2 * kPairs; kb < kNHBlk - 1; ++kb) {
-    const bool refill = kb < kRefill;
-    const int ahead = min(C::kStages - 2, kNHBlk - 2 - kb);
-    if (kb & 1)
-      step(kb, f1, f0, ahead, refill);
-    else
-      step(kb, f0, f1, ahead, refill);
+    for (int mi = 0; mi < MI; ++mi) read_a(kb, mi, f);
+    compute(f);
   }
-  compute(((kNHBlk - 1) & 1) ? f1 : f0);
 
   // ---- SwiGLU epilogue (moe.py:190-193): act = silu(up) * gate ------------
 #pragma unroll
