@@ -299,8 +299,8 @@ def cpu_time(pkg, torch, wl):
 
 def measured_peaks(pkg, torch, dev):
     """Roofline denominators measured on this GPU: a streaming read of 4 GiB
-    (16-byte loads, every byte once) and MFMA loops of the two instructions
-    the GEMMs use (operands in registers, 8 waves per CU)."""
+    (16-byte nontemporal loads, every byte once) and MFMA loops of the two
+    instructions the GEMMs use (operands in registers, 16 waves per CU)."""
     import ctypes
 
     L = pkg._lib.bench_lib()
@@ -322,19 +322,26 @@ def measured_peaks(pkg, torch, dev):
 
     nbytes = 4 << 30
     buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(3)
-    blocks = cus * 16
-    sink = torch.empty(blocks * 512, dtype=torch.float32, device=dev)
-    rd = timed(lambda: L.moe_bench_read_stream(ctypes.c_void_p(buf.data_ptr()), nbytes,
-                                               ctypes.c_void_p(sink.data_ptr()), blocks, stream))
+    blocks = cus * 4
+    mfma_blocks = 2 * cus  # 16 waves per CU: 8 per CU leave the MFMA pipes 10-15% idle
+    sink = torch.empty(max(blocks * 256, mfma_blocks * 512), dtype=torch.float32, device=dev)
+
+    def read():
+        rc = L.moe_bench_read_stream(ctypes.c_void_p(buf.data_ptr()), nbytes, ctypes.c_void_p(sink.data_ptr()),
+                                     blocks, stream)
+        assert rc == 0, f"moe_bench_read_stream: hipError {rc}"
+
+    rd = timed(read)
     del buf
     out = {"hbm_read_GBps": round(nbytes / rd / 1e9, 1)}
     for kind, name, k in ((0, "mfma_fp8_TFLOPs", 128), (1, "mfma_bf16_TFLOPs", 32)):
         iters = 4000
-        t = timed(lambda: L.moe_bench_mfma_loop(kind, iters, cus, ctypes.c_void_p(sink.data_ptr()), stream))
-        flops = cus * 8 * iters * 8 * 2 * 16 * 16 * k
+        t = timed(lambda: L.moe_bench_mfma_loop(kind, iters, mfma_blocks, ctypes.c_void_p(sink.data_ptr()), stream))
+        flops = mfma_blocks * 8 * iters * 8 * 2 * 16 * 16 * k
         out[name] = round(flops / t / 1e12, 1)
-    out["method"] = ("streaming read of 4 GiB with 16-byte loads; MFMA loops of v_mfma_f32_16x16x128_f8f6f4 / "
-                     "v_mfma_f32_16x16x32_bf16, 8 independent accumulators per wave, 8 waves per CU "
+    out["method"] = ("streaming read of 4 GiB, one contiguous chunk per workgroup, 16-byte nontemporal loads; "
+                     "MFMA loops of v_mfma_f32_16x16x128_f8f6f4 / "
+                     "v_mfma_f32_16x16x32_bf16, 8 independent accumulators per wave, 16 waves per CU "
                      "(lib/libmoe_bench.so, csrc/peaks.hip)")
     log(f"[bench] measured peaks: {out}")
     return out

@@ -149,7 +149,7 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
       const uint8_t* src = w13 + n * kH + kb0 * kBlk + 16 * c;
 #pragma unroll
       for (int j = 0; j < kS1KB; ++j)
-        if ((j < kS1CopySplit) == (part == 0)) dma16(src + j * kBlk, wbuf + (2 * j + h) * 1024);
+        if ((j < kS1CopySplit) == (part == 0)) dma16_nt(src + j * kBlk, wbuf + (2 * j + h) * 1024);
     }
   };
   // Row tile rt of an item: token of this lane's A row (kDirect: the rows

@@ -107,7 +107,7 @@ __device__ __forceinline__ void s2_copy_w(char* stage, S2Job j, const uint8_t* _
       wide_copy_lane(lane, h, r, c);
       const uint8_t* src = w2 + ((size_t)j.e * kH + n0 + 16 * nb + r) * kI + kb0 * kBlk + 16 * c;
 #pragma unroll
-      for (int k = 0; k < kS2KB; ++k) dma16(src + k * kBlk, stage + ((nb * kS2KB + k) * 2 + h) * 1024);
+      for (int k = 0; k < kS2KB; ++k) dma16_nt(src + k * kBlk, stage + ((nb * kS2KB + k) * 2 + h) * 1024);
     }
 }
 

@@ -231,6 +231,13 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ void dma16(const void* g, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_wave_base, 16, 0, 0);
 }
+// Same with the nontemporal (nt) cache policy, for data read exactly once:
+// the streaming kernels' expert weights (small_t64: GEMM1 101 -> 87 us).  The
+// tiled kernels re-read weight tiles through L2 and keep dma16 (nt there made
+// GEMM2 at T = 8192 34% slower).
+__device__ __forceinline__ void dma16_nt(const void* g, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_wave_base, 16, 0, 2);
+}
 // Same with 4 bytes per lane (global_load_lds_dword): lane i -> base + 4 * i.
 __device__ __forceinline__ void dma4(const void* g, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_void*)lds_wave_base, 4, 0, 0);
