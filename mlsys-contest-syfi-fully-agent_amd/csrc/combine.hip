@@ -19,7 +19,8 @@ namespace {
 // 896 threads x 8 columns = one 7168-column row per workgroup; every lane
 // issues its (up to 8 rows x 2) 16-byte loads of fp32 GEMM2 rows before the
 // first add.  Thread i takes columns 4i .. 4i+3 and 3584 + 4i .. +3, so each
-// load instruction of a wave covers 1 KB of contiguous bytes.
+// load instruction of a wave covers 1 KB of contiguous bytes.  The rows are
+// read once, with nontemporal loads (at T = 8192: 201 -> 183 us).
 constexpr int kCombThreads = 896;
 constexpr int kCombHalf = kH / 2;
 static_assert(kCombThreads * 4 == kCombHalf, "one row per workgroup");
@@ -41,8 +42,8 @@ combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_
   for (int k = 0; k < kTopK; ++k) {
     const float* src = down + (size_t)max(row[k], 0) * kH;
     if (row[k] >= 0) {
-      v[k][0] = *(const v4f*)(src + c[0]);
-      v[k][1] = *(const v4f*)(src + c[1]);
+      v[k][0] = __builtin_nontemporal_load((const v4f*)(src + c[0]));
+      v[k][1] = __builtin_nontemporal_load((const v4f*)(src + c[1]));
     }
   }
   // ascending expert order, acc = acc + (O * w): two roundings, as index_add_

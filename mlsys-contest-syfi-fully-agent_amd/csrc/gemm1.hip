@@ -55,7 +55,8 @@ constexpr int kS1CopyOps1 = 2 * (kS1KB - kS1CopySplit);  // copies per lane, par
 struct S1TileOps {
   v8i a[kS1KB];     // A rows (token rows of hidden_states), this wave's K range
   float s0, s1;     // two of the tile's activation scale entries (lane l: l and 64 + l)
-  float sw[kS1KB];  // weight block scales of this lane's column
+  float sg[kS1KB];  // weight block scales of the item's gate rows (scalar loads) ...
+  float su[kS1KB];  // ... and of its up rows; lane r < 8 takes sg, r >= 8 su
   int ptok;         // kDirect: token of the expert's permuted row threadIdx.x (< M)
 };
 
@@ -168,9 +169,12 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     o.ptok = 0;
     if (kDirect && (int)threadIdx.x < X.end(e) - X.begin(e)) o.ptok = ptok_src[X.begin(e) + threadIdx.x];
   };
-  // The item's weight block scales (this lane's column): the gate rows and
-  // the up rows of an item lie in one 128-row scale block each, so the loads
-  // are wave-uniform (scalar loads, counted by lgkmcnt, not vmcnt).
+  // The item's weight block scales: the gate rows and the up rows of an item
+  // lie in one 128-row scale block each, so the loads are wave-uniform
+  // (scalar loads, counted by lgkmcnt, not vmcnt).  They are issued after
+  // the item's weight copies and each lane picks its column's scale only in
+  // compute_tile, so no wait for them holds up the copies (small_t64: GEMM1
+  // 89 -> 87 us).
   auto issue_sw = [&](int item, S1TileOps& o) {
     const int cg = item % kS1Groups;
     const int e = nth_set_bit(active, item / kS1Groups);
@@ -178,8 +182,8 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     const float* su = w13_scale + (((size_t)e * k2I + kI + 8 * cg) / kBlk) * kNHBlk + kb0;
 #pragma unroll
     for (int j = 0; j < kS1KB; ++j) {
-      const float g = sg[j], u = su[j];
-      o.sw[j] = lr < 8 ? g : u;
+      o.sg[j] = sg[j];
+      o.su[j] = su[j];
     }
   };
   // Multiply a landed tile, reduce the 8 K-partials in a fixed order, SwiGLU,
@@ -201,8 +205,9 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     for (int j = 0; j < kS1KB; ++j) {
       const v4f p = mfma_f8_16x16x128(o.a[j], b[j]);
       const v4f sc = *(const v4f*)&sa[j * 16 + 4 * lq];
+      const float sw = lr < 8 ? o.sg[j] : o.su[j];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], sc[i] * o.sw[j], acc[i]);
+      for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], sc[i] * sw, acc[i]);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * kWave + lane] = acc[i];
@@ -246,9 +251,9 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
   S1Out pend;       // the previous tile's outputs, stored once the next loads are out
   if (i0 < i1) {
     issue_rows(i0, 0, cur);
-    issue_sw(i0, cur);
     copy_w(i0, 0);
     copy_w(i0, 1);
+    issue_sw(i0, cur);
   }
   // fragment of block j: lane (q, r) holds row r, K bytes 32q .. 32q+31
   const int slot_lo = wide_slot(lr, 2 * lq), slot_hi = wide_slot(lr, 2 * lq + 1);
@@ -275,9 +280,9 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // part 0 is read: free for the next item's
     S1TileOps nxt = cur;
     if (more) {
-      issue_sw(item + 1, nxt);
       if (new_rows) issue_rows(item + 1, 0, nxt);
       copy_w(item + 1, 0);
+      issue_sw(item + 1, nxt);
     }
     // Part 1 has landed; the next item's part 0 may still be in flight (after
     // new row operands, whose load count is not fixed, everything is waited
@@ -300,7 +305,10 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
         S1TileOps o;
         issue_rows(item, rt, o);
 #pragma unroll
-        for (int j = 0; j < kS1KB; ++j) o.sw[j] = cur.sw[j];
+        for (int j = 0; j < kS1KB; ++j) {
+          o.sg[j] = cur.sg[j];
+          o.su[j] = cur.su[j];
+        }
         wait_vmcnt_lgkm0<0>();  // also the next item's copy: experts of > 16 rows are rare here
         asm volatile("" ::: "memory");
         store_out(item, pend);
