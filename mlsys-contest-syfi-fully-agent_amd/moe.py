@@ -36,9 +36,15 @@ _ws: dict = {}
 
 
 def workspace(device: torch.device, T: int) -> torch.Tensor:
-    """Per-device workspace, grown on demand (needs no initialisation)."""
+    """Workspace of the current stream of `device`, grown on demand (needs no
+    initialisation).  One buffer per (device, stream): calls on different
+    streams never share one (the C entry points need distinct workspaces for
+    concurrent calls), and a buffer is allocated on the stream that uses it,
+    so when it grows, torch's caching allocator hands the old memory out
+    again only to later work on that same stream."""
     need = _lib.moe_lib().moe_fp8_ds_workspace_size(T)
-    key = (device.type, device.index)
+    stream = torch.cuda.current_stream(device)
+    key = (device.type, device.index, stream.cuda_stream)
     with _ws_lock:
         buf = _ws.get(key)
         if buf is None or buf.numel() < need:

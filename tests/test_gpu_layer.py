@@ -192,6 +192,31 @@ def test_workspace_needs_no_initialisation(pkg, cuda_device):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
 
 
+def test_concurrent_streams_use_their_own_workspaces(pkg, cuda_device):
+    """Calls on two streams at once (different T, so each one's workspace
+    holds different intermediates) give the bits of the same calls made one
+    after the other, and each stream has its own workspace."""
+    cfg = pkg.synth.CONFIGS["prefill_t1024"]
+    w, _ = gpu_weights(pkg, cfg.seed, cuda_device)
+    toks = [gpu_tokens(pkg, cfg, cuda_device, T)[0] for T in (300, 96)]
+    want = [run_layer(pkg, tok, w, cfg.local_expert_offset, cfg.routed_scaling_factor) for tok in toks]
+    streams = [torch.cuda.Stream(device=cuda_device) for _ in toks]
+    outs = [torch.full((tok[0].shape[0], H), float("nan"), dtype=torch.bfloat16, device=cuda_device) for tok in toks]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for s, tok, out in zip(streams, toks, outs):
+            with torch.cuda.stream(s):
+                pkg.run(*tok, *w, cfg.local_expert_offset, cfg.routed_scaling_factor, out)
+    torch.cuda.synchronize()
+    for got, ref in zip(outs, want):
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    ptrs = []
+    for s, tok in zip(streams, toks):
+        with torch.cuda.stream(s):
+            ptrs.append(pkg.workspace(cuda_device, tok[0].shape[0]).data_ptr())
+    assert ptrs[0] != ptrs[1]
+
+
 def test_synth_matches_cpu_generator(pkg, orc, cuda_device):
     """The GPU generator writes the same bytes as the oracle's CPU generator."""
     for name in ("plumbing_t16", "skewed_t8192"):
