@@ -9,7 +9,8 @@ import os
 
 _DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(_DIR, "lib")
-MOE_LIB = os.path.join(LIB_DIR, "libmoe_fp8_ds.so")
+# MOE_FP8_DS_LIB names another build of the same library (the tests' host-sanitized one)
+MOE_LIB = os.environ.get("MOE_FP8_DS_LIB") or os.path.join(LIB_DIR, "libmoe_fp8_ds.so")
 SYNTH_LIB = os.path.join(LIB_DIR, "libmoe_synth.so")
 BENCH_LIB = os.path.join(LIB_DIR, "libmoe_bench.so")
 

@@ -20,7 +20,8 @@ H, I, E_LOCAL, E_GLOBAL, TOP_K, BLOCK = 7168, 2048, 32, 256, 8, 128
 NH_BLK, NI_BLK, N2I_BLK = H // BLOCK, I // BLOCK, 2 * I // BLOCK
 
 _DIR = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_DIR, "_build", "liboracle.so")
+# MOE_ORACLE_LIB names another build of the same library (the tests' host-sanitized one)
+_LIB_PATH = os.environ.get("MOE_ORACLE_LIB") or os.path.join(_DIR, "_build", "liboracle.so")
 _lib = None
 
 
