@@ -349,12 +349,15 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = P[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
   for (int s = 0; s < C::kStages - 1; ++s) issue(s);
-#pragma unroll 1
-  for (int s = 0; s < C::kSteps; ++s) {
+  // Two steps (one 128-K weight scale block) per iteration: the block's
+  // first MFMAs start from a zero accumulator, the second step's results are
+  // scaled into acc.
+  static_assert(C::kSteps % 2 == 0, "steps pair into scale blocks");
+  auto step = [&](int s, bool first) {
     // stages s+1 .. s+kStages-2 may stay in flight
     wait_stages_ahead<C::kPlanesPerWave>(min(C::kSteps - 1 - s, C::kStages - 2));
     block_barrier();
@@ -380,22 +383,25 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int nj = 0; nj < NJ; ++nj) {
-        P[mi][nj] = mfma_bf16_16x16x32(a[mi][0], b[nj][0], P[mi][nj]);
+        P[mi][nj] = mfma_bf16_16x16x32(a[mi][0], b[nj][0], first ? v4f{0.f, 0.f, 0.f, 0.f} : P[mi][nj]);
         P[mi][nj] = mfma_bf16_16x16x32(a[mi][1], b[nj][1], P[mi][nj]);
         P[mi][nj] = mfma_bf16_16x16x32(al[mi][0], b[nj][0], P[mi][nj]);
         P[mi][nj] = mfma_bf16_16x16x32(al[mi][1], b[nj][1], P[mi][nj]);
       }
-    if (s & 1) {
+    if (!first) {
       const float sb = wsc[wn * kNIBlk + (s >> 1)];
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int nj = 0; nj < NJ; ++nj) {
+        for (int nj = 0; nj < NJ; ++nj)
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[mi][nj][i] = __builtin_fmaf(P[mi][nj][i], sb, acc[mi][nj][i]);
-          P[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
-        }
     }
+  };
+#pragma unroll 1
+  for (int s = 0; s < C::kSteps; s += 2) {
+    step(s, true);
+    step(s + 1, false);
   }
 
 #pragma unroll
