@@ -258,6 +258,67 @@ def measured_traffic(workload, stage):
     return None, None
 
 
+# kernel-name prefix -> bench stage (the layer's kernels only)
+_STAGE_OF = (("route", "route"), ("perm", "route"), ("gemm1", "gemm1_swiglu"), ("gemm2", "gemm2"),
+             ("combine", "combine"))
+
+
+def live_traffic(workload, timeout_s=180):
+    """HBM bytes per launch of every stage of `workload`, measured in this
+    bench run: two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE; one
+    counter group each) over child runs of this script (--calls-only plus a
+    1 GiB device copy), each scaled so that the copy reads and writes exactly
+    1 GiB.  Called before this process touches the GPU.  Returns
+    ({stage: bytes}, None) or (None, reason)."""
+    import csv
+    import glob
+    import re
+    import shutil
+    import subprocess
+    import tempfile
+
+    if shutil.which("rocprofv3") is None:
+        return None, "rocprofv3 not found"
+    tmp = tempfile.mkdtemp(prefix="moe_bench_pmc_")
+    env = dict(os.environ, TMPDIR="/tmp")
+    per_stage = {}
+    try:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            out = os.path.join(tmp, counter)
+            cmd = ["timeout", "-s", "KILL", str(timeout_s), "rocprofv3", "--pmc", counter, "--output-format", "csv",
+                   "-d", out, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-quant",
+                   "--no-peaks", "--no-traffic", "--sweep", "", "--workload", workload, "--calls-only", "--steps", "3",
+                   "--warmup", "1", "--copy-calib-mib", "1024"]
+            log(f"[bench] traffic: rocprofv3 --pmc {counter} pass on {workload}")
+            r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
+            files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+            if not files:
+                return None, f"rocprofv3 --pmc {counter} wrote no counters (exit {r.returncode})"
+            sums, calib, calib_id = {}, None, -1
+            for f in files:
+                for row in csv.DictReader(open(f)):
+                    name = row["Kernel_Name"]
+                    val = float(row["Counter_Value"])
+                    if "copyBuffer" in name:  # the last one is the 1 GiB calibration copy
+                        did = int(row["Dispatch_Id"])
+                        if did > calib_id:
+                            calib_id, calib = did, val
+                        continue
+                    short = re.sub(r"^void ", "", name.replace("moe::(anonymous namespace)::", ""))
+                    for prefix, stage in _STAGE_OF:
+                        if short.startswith(prefix):
+                            key = (stage, short.split("(")[0])
+                            sums.setdefault(key, []).append(val)
+            if not calib:
+                return None, f"no calibration copy in the {counter} pass"
+            scale = 1024.0 * (1048576.0 / calib)  # KiB -> bytes, then the copy's 1 GiB
+            for (stage, _), vals in sums.items():  # mean per dispatch, summed over a stage's kernels
+                per_stage[stage] = per_stage.get(stage, 0.0) + scale * sum(vals) / len(vals)
+        return {k: int(v) for k, v in per_stage.items()}, None
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def copy_calibration(torch, dev, mib):
     """A plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE
     counters of a --pmc run of this script."""
@@ -400,6 +461,9 @@ def main():
     ap.add_argument("--no-peaks", action="store_true", help="skip the measured-peak microbenchmarks")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this size (for PMC byte calibration)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="take roofline.traffic from the committed counter summaries instead of two live "
+                         "rocprofv3 --pmc passes")
     ap.add_argument("--calls-only", action="store_true",
                     help="only the headline's plain calls (no graphs, no events): for rocprofv3 --pmc runs")
     args = ap.parse_args()
@@ -408,6 +472,11 @@ def main():
         print("bench.py: this build runs on one GPU only (the layer is one expert-parallel rank's "
               "shard; no collectives are implemented). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    # HBM traffic first, from child processes, before this process touches the GPU
+    live, live_err = (None, "--no-traffic") if (args.no_traffic or args.calls_only) else live_traffic(args.workload)
+    if live_err and not args.calls_only:
+        log(f"[bench] traffic: live measurement unavailable ({live_err}); using the committed summaries")
 
     import torch
 
@@ -466,12 +535,19 @@ def main():
                                   f"{threads} host threads; measured, not extrapolated")}
 
     dom = hm["dominant"]
-    traffic, traffic_src = measured_traffic(args.workload, dom["kernel"])
+    if live and dom["kernel"] in live:
+        traffic = live[dom["kernel"]]
+        traffic_src = ("measured in this run: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes (child runs of "
+                       "bench.py --calls-only), each scaled by a 1 GiB device copy in the same pass")
+    else:
+        traffic, path = measured_traffic(args.workload, dom["kernel"])
+        traffic_src = (f"{path}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run of this bench, copy-calibrated "
+                       f"(not measured in this run: {live_err})") if path else None
     roof = {"bound": dom["bound"], "achieved": round(dom["achieved"], 3), "peak": dom["peak"],
             "unit": dom["unit"], "frac": round(dom["frac"], 4), "traffic": traffic,
-            "traffic_source": (f"{traffic_src}: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run of this bench, "
-                               f"copy-calibrated (not measured in this run)") if traffic_src else None,
-            "kernel": dom["kernel"], "kernel_us": round(dom["ms"] * 1e3, 3)}
+            "traffic_source": traffic_src, "kernel": dom["kernel"], "kernel_us": round(dom["ms"] * 1e3, 3)}
+    if live:
+        roof["traffic_by_stage"] = live
     if dom["kernel"] == "gemm2":
         # the activation enters as a bf16 (hi, lo) pair: two bf16 MFMAs per product
         roof["mfma_flops_executed"] = 2 * dom["algo_flops"]
