@@ -168,6 +168,10 @@ struct SmallRoute {
   float pair_w[kSmallRouteMaxTokens][kTopK];       // their weights
   int perm_token[kSmallRouteMaxTokens * kTopK];    // token of each permuted row
   float perm_w[kSmallRouteMaxTokens * kTopK];      // weight of each permuted row
+  // T == 1 (route_one): the token's 32-bit keys, sigmoid scores and group scores
+  uint32_t key1[kEGlobal];
+  float s1[kEGlobal];
+  float g1[kNGroup];
 };
 
 struct RouteOut {
@@ -179,8 +183,156 @@ struct RouteOut {
   float* perm_w;
 };
 
+// T == 1: the same routing as route_token, with the work of one token spread
+// over four waves (waves 0-3 each compute one 64-expert slot's keys and its
+// two group scores) and the top-8 over the 128 experts of the kept groups
+// only (two keys per lane in wave 0), then the permutation of the single
+// token written directly.  Needs at least 4 waves; ends with a workgroup
+// barrier.
+__device__ inline void route_one(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf,
+                                 int64_t offset, SmallRoute& sr, RouteOut out, bool write_out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  if (wave < 4) {
+    const int e = 64 * wave + lane;
+    const float x = logits[e];
+    // moe.py:127-128 (as route_token): exp in double, rounded once; biased score
+    const float ex = (float)exp(-(double)x);
+    const float sv = 1.0f / (1.0f + ex);
+    const uint32_t key = float_order_key(sv + bf16_to_f32(bias[e]));
+    sr.s1[e] = sv;
+    sr.key1[e] = key;
+    // moe.py:135-136: the slot's two groups (half-waves), top-2 sums
+    uint32_t a0, b0, a1, b1;
+    halfwave_top2(key, a0, b0, a1, b1);
+    if (lane == 0) {
+      sr.g1[2 * wave] = float_from_order_key(a0) + float_from_order_key(b0);
+      sr.g1[2 * wave + 1] = float_from_order_key(a1) + float_from_order_key(b1);
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // moe.py:139-146: keep the top-4 groups (ties -> lower group index)
+    float G[kNGroup];
+#pragma unroll
+    for (int g = 0; g < kNGroup; ++g) G[g] = sr.g1[g];
+    uint32_t keep = 0;
+#pragma unroll
+    for (int g = 0; g < kNGroup; ++g) {
+      int rank = 0;
+#pragma unroll
+      for (int h = 0; h < kNGroup; ++h) rank += (G[h] > G[g]) || (G[h] == G[g] && h < g);
+      keep |= (rank < kTopKGroup ? 1u : 0u) << g;
+    }
+    // Candidates: lane l holds expert 32 kg[l/32] + l%32 (slot 0) and
+    // 32 kg[2 + l/32] + l%32 (slot 1), kg the kept groups ascending, so
+    // (slot, lane) order is expert order.  Exactly four groups are kept
+    // unless group scores are NaN; then, and when a kept key is 0 (the key
+    // route_token gives dropped experts), route_token's own selection runs.
+    int kg[kTopKGroup];
+    uint32_t m = keep;
+#pragma unroll
+    for (int k = 0; k < kTopKGroup; ++k) {
+      kg[k] = m ? __builtin_ctz(m) : 0;
+      m &= m - 1;
+    }
+    const int half = lane >> 5;
+    const int ea = 32 * (half ? kg[1] : kg[0]) + (lane & 31), eb = 32 * (half ? kg[3] : kg[2]) + (lane & 31);
+    uint32_t key[2] = {sr.key1[ea], sr.key1[eb]};
+    const bool plain = __popc(keep) == kTopKGroup && !__ballot(key[0] == 0u || key[1] == 0u);
+    int pick[kTopK];
+    float wsel[kTopK];
+    if (plain) {
+      // moe.py:149-151: eight rounds of (wave maximum, lowest expert holding it)
+#pragma unroll
+      for (int r = 0; r < kTopK; ++r) {
+        const uint32_t M = wave_max_u32(max(key[0], key[1]));
+        const uint64_t b0 = __ballot(key[0] == M), b1 = __ballot(key[1] == M);
+        const int l = b0 ? __builtin_ctzll(b0) : __builtin_ctzll(b1);
+        const int slot = b0 ? 0 : 1;
+        const int hl = l >> 5;
+        pick[r] = 32 * (slot ? (hl ? kg[3] : kg[2]) : (hl ? kg[1] : kg[0])) + (l & 31);
+        if (lane == l) key[slot] = 0u;  // taken (no candidate key is 0)
+      }
+      constexpr int kNet[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
+                                   {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+      for (int c = 0; c < 19; ++c) {
+        const int x0 = pick[kNet[c][0]], y0 = pick[kNet[c][1]];
+        pick[kNet[c][0]] = min(x0, y0);
+        pick[kNet[c][1]] = max(x0, y0);
+      }
+      // moe.py:154-158: un-biased scores, summed in ascending id order,
+      // normalised (true division) then scaled -- as route_token
+#pragma unroll
+      for (int r = 0; r < kTopK; ++r) wsel[r] = sr.s1[pick[r]];
+      float sum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kTopK; ++k) sum = sum + wsel[k];
+      const float denom = sum + 1e-20f;
+#pragma unroll
+      for (int k = 0; k < kTopK; ++k) wsel[k] = (wsel[k] / denom) * rsf;
+    } else {
+      route_token(logits, bias, rsf, 0, pick, wsel);
+    }
+    // moe.py:168-179 for one token: its local experts, ascending, take rows
+    // 0, 1, ...; expert_off[le] counts the local picks below le
+    int row_of[kTopK];
+    int rows = 0;
+#pragma unroll
+    for (int r = 0; r < kTopK; ++r) {
+      const int64_t le = (int64_t)pick[r] - offset;
+      row_of[r] = (le >= 0 && le < kELocal) ? rows++ : -1;
+    }
+    if (lane <= kELocal) {
+      int below = 0;
+      uint32_t mine = 0u;
+#pragma unroll
+      for (int r = 0; r < kTopK; ++r) {
+        const int64_t le = (int64_t)pick[r] - offset;
+        if (row_of[r] >= 0 && le < lane) ++below;
+        if (row_of[r] >= 0 && le == lane) mine = 1u;
+      }
+      sr.expert_off[lane] = below;
+      if (write_out) out.expert_off[lane] = below;
+      if (lane < kELocal) sr.tokmask[lane] = mine;
+    }
+    if (lane < kTopK) {
+      int e = pick[0], row = row_of[0];
+      float we = wsel[0];
+#pragma unroll
+      for (int r = 1; r < kTopK; ++r)
+        if (lane == r) {
+          e = pick[r];
+          row = row_of[r];
+          we = wsel[r];
+        }
+      sr.pair_id[0][lane] = e;
+      sr.pair_w[0][lane] = we;
+      if (row >= 0) {
+        sr.perm_token[row] = 0;
+        sr.perm_w[row] = we;
+      }
+      if (write_out) {
+        out.ids[lane] = e;
+        out.w[lane] = we;
+        out.pair_row[lane] = row;
+        if (row >= 0) {
+          out.perm_token[row] = 0;
+          out.perm_w[row] = we;
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
 __device__ inline void route_small(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf,
                                    int T, int64_t offset, SmallRoute& sr, RouteOut out, bool write_out) {
+  if (T == 1) {
+    route_one(logits, bias, rsf, offset, sr, out, write_out);
+    return;
+  }
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int waves = blockDim.x / kWave;
