@@ -142,24 +142,30 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
   // Jobs in ascending (expert, row tile) order.  The W2 slices of the next
   // two jobs stream into the wave's two LDS stages while one is multiplied;
   // the act rows of the next job load into registers.
+  //
+  // Act rows are loaded only together with a W2 copy after them (when no job
+  // after next exists, a second copy of the job just copied, whose lines are
+  // in flight or in L2), so the act rows of every job are older than the
+  // last 8 loads when its step starts.  The compiler's own wait before the
+  // MFMAs counts, along every path, the loads issued after the operands';
+  // with a copy that could be skipped alone it merged the paths to vmcnt(0)
+  // and so waited for the prefetch it had just issued, one full memory
+  // latency per job (small_t64: 3.6 us per job, 2.1 of it that wait).
   S2Job job = s2_next(X, active, {-1, 0});
   S2Job j1 = job.e >= 0 ? s2_next(X, active, job) : job;
   S2Regs r0, r1;
   if (job.e >= 0) {
     s2_load(r0, job, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
     s2_copy_w(stage(0), job, w2, n0, kb0, lane);
+    s2_copy_w(stage(1), j1.e >= 0 ? j1 : job, w2, n0, kb0, lane);
   }
-  if (j1.e >= 0) s2_copy_w(stage(1), j1, w2, n0, kb0, lane);
   // One job from stage `s` with act rows `cur`; loads the next job's act rows
   // into `nxt` and starts the copy of the job after next into stage `s`.
   // Issue order is always: act rows of job j, copy of job j + 1.
   auto step = [&](int s, const S2Regs& cur, S2Regs& nxt) {
     // This job's W2 stage and act rows have landed; the next job's W2 copy
     // (8 per lane, issued last) may stay in flight.
-    if (j1.e >= 0)
-      wait_vmcnt_lgkm0<2 * kS2KB * kS2NB>();
-    else
-      wait_vmcnt_lgkm0<0>();
+    wait_vmcnt_lgkm0<2 * kS2KB * kS2NB>();
     asm volatile("" ::: "memory");
     v4i b[kS2NB][kS2KB][2];
 #pragma unroll
@@ -171,8 +177,10 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
           b[nb][k][g] = *(const v4i*)(stage(s) + 2 * (nb * kS2KB + k) * 1024 + wide_slot(lr, 4 * g + lq));
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the stage is read: free for the job after next
     const S2Job j2 = j1.e >= 0 ? s2_next(X, active, j1) : j1;
-    if (j1.e >= 0) s2_load(nxt, j1, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
-    if (j2.e >= 0) s2_copy_w(stage(s), j2, w2, n0, kb0, lane);
+    if (j1.e >= 0) {
+      s2_load(nxt, j1, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
+      s2_copy_w(stage(s), j2.e >= 0 ? j2 : j1, w2, n0, kb0, lane);
+    }
 #pragma unroll
     for (int nb = 0; nb < kS2NB; ++nb) {
       v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -219,6 +227,7 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
     if (job.e < 0) break;
     step(1, r1, r0);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated copy lands before the LDS is released
   for (int i = threadIdx.x; i < T * kS2Cols; i += kS2Threads)
     out[(size_t)(i / kS2Cols) * kH + n0 + (i % kS2Cols)] = f32_to_bf16_rne(outacc[i]);
 }
