@@ -166,8 +166,13 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     const uint8_t* ap = hs + (size_t)tok * kH + kb0 * kBlk + 32 * lq;
 #pragma unroll
     for (int j = 0; j < kS1KB; ++j) o.a[j] = *(const v8i*)(ap + j * kBlk);
+  };
+  // kDirect: the expert's permutation entries (LDS), the only per-expert
+  // part of the row operands
+  auto read_ptok = [&](int item, S1TileOps& o) {
+    const int e = nth_set_bit(active, item / kS1Groups);
     o.ptok = 0;
-    if (kDirect && (int)threadIdx.x < X.end(e) - X.begin(e)) o.ptok = ptok_src[X.begin(e) + threadIdx.x];
+    if ((int)threadIdx.x < X.end(e) - X.begin(e)) o.ptok = ptok_src[X.begin(e) + threadIdx.x];
   };
   // The item's weight block scales: the gate rows and the up rows of an item
   // lie in one 128-row scale block each, so the loads are wave-uniform
@@ -247,10 +252,21 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
   const int per = (items + (int)gridDim.x - 1) / (int)gridDim.x;
   const int i0 = blockIdx.x * per;
   const int i1 = min(items, i0 + per);
+  // One set of operands.  The weight scales of the next item are scalar
+  // loads into `nsw` while an item runs.  The row operands change only with
+  // the expert (kDirect: never -- the rows are the T tokens for every
+  // expert, only the permutation entries change) and are then reloaded
+  // after the item's tiles, and waited for at once: once per expert change
+  // (or per item, for an expert of more than 16 rows, whose later row tiles
+  // pass through the same registers).  A second set filled while the item
+  // runs and copied over at its end made the compiler wait at every item
+  // for every load, the next item's whole weight copy included, since it
+  // could not tell the copied registers had landed.
   S1TileOps cur;
   S1Out pend;       // the previous tile's outputs, stored once the next loads are out
   if (i0 < i1) {
     issue_rows(i0, 0, cur);
+    if (kDirect) read_ptok(i0, cur);
     copy_w(i0, 0);
     copy_w(i0, 1);
     issue_sw(i0, cur);
@@ -262,10 +278,10 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     const v4i hi = *(const v4i*)(wbuf + 2 * j * 1024 + slot_hi);
     b[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
-  // Vector-memory order per item: [row operands, only when the expert
-  // changes] [copy part 0] ... [copy part 1] [the previous tile's store].
-  // The weight scales are scalar loads (lgkmcnt), so outside an expert change
-  // only copies and at most one store are counted.
+  // Vector-memory order per item: [copy part 0] ... [copy part 1] [the
+  // previous tile's store], then on an expert change the next row operands,
+  // waited for at once.  The weight scales are scalar loads (lgkmcnt), so
+  // only copies and at most one store are counted by the waits below.
 #pragma unroll 1
   for (int item = i0; item < i1; ++item) {
     const bool more = item + 1 < i1;
@@ -278,16 +294,13 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
 #pragma unroll
     for (int j = 0; j < kS1CopySplit; ++j) read_b(b, j);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // part 0 is read: free for the next item's
-    S1TileOps nxt = cur;
+    S1TileOps nsw;  // the next item's weight scales (only sg, su are used)
     if (more) {
-      if (new_rows) issue_rows(item + 1, 0, nxt);
       copy_w(item + 1, 0);
-      issue_sw(item + 1, nxt);
+      issue_sw(item + 1, nsw);
     }
-    // Part 1 has landed; the next item's part 0 may still be in flight (after
-    // new row operands, whose load count is not fixed, everything is waited
-    // for: once per expert change).
-    if (more && !new_rows)
+    // Part 1 has landed; the next item's part 0 may still be in flight.
+    if (more)
       wait_vmcnt_lgkm0<kS1CopyOps0>();
     else
       wait_vmcnt_lgkm0<0>();
@@ -298,24 +311,32 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     if (more) copy_w(item + 1, 1);
     if (item != i0) store_out(item - 1, pend);
     compute_tile(item, 0, cur, b, pend);
-    if (!kDirect) {
+    if (kDirect) {
+      if (new_rows) read_ptok(item + 1, cur);
+    } else {
       const int e = nth_set_bit(active, item / kS1Groups);
+      const bool multi_tile = X.end(e) - X.begin(e) > 16;
 #pragma unroll 1
       for (int rt = 1; rt * 16 < X.end(e) - X.begin(e); ++rt) {
-        S1TileOps o;
-        issue_rows(item, rt, o);
-#pragma unroll
-        for (int j = 0; j < kS1KB; ++j) {
-          o.sg[j] = cur.sg[j];
-          o.su[j] = cur.su[j];
-        }
+        issue_rows(item, rt, cur);
         wait_vmcnt_lgkm0<0>();  // also the next item's copy: experts of > 16 rows are rare here
         asm volatile("" ::: "memory");
         store_out(item, pend);
-        compute_tile(item, rt, o, b, pend);
+        compute_tile(item, rt, cur, b, pend);
+      }
+      if (more && (new_rows || multi_tile)) {
+        issue_rows(item + 1, 0, cur);
+        wait_vmcnt_lgkm0<0>();
+        asm volatile("" ::: "memory");
       }
     }
-    cur = nxt;
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < kS1KB; ++j) {
+        cur.sg[j] = nsw.sg[j];
+        cur.su[j] = nsw.su[j];
+      }
+    }
   }
   if (i0 < i1) store_out(i1 - 1, pend);
 }

@@ -46,6 +46,10 @@ LAYER_CASES = [
     ("prefill_t1024", 256, 128, None),
     # token counts on either side of each kernel-choice boundary
     ("small_t64", None, 17, None),        # first T past the in-GEMM1 routing
+    # streaming kernels with experts of more than 16 rows (four hot experts of
+    # up to 64 and 40 rows: the row-tile loops)
+    ("skewed_t8192", None, 64, None),
+    ("skewed_t8192", None, 40, None),
     ("prefill_t1024", None, 65, None),    # first T with the tiled GEMM1 and a combine pass
     ("skewed_t8192", None, 1024, None),   # largest T of the tiled GEMM1
     ("skewed_t8192", None, 1025, None),   # smallest T of the wide GEMM1
@@ -113,6 +117,7 @@ def test_layer_matches_reference_golden(pkg, cuda_device, name):
 
 INTERMEDIATE_CASES = [
     ("small_t64", None, None),          # row-streaming kernels
+    ("skewed_t8192", 64, None),         # row-streaming kernels, experts of up to 64 rows
     ("prefill_t1024", None, 200),
     ("skewed_t8192", 2304, 160),        # LDS-tiled / wide kernels, ragged last tiles
 ]
