@@ -203,7 +203,7 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     if (kDirect) {
       if (threadIdx.x < 16) inv[threadIdx.x] = -1;
       lds_barrier();
-      if (threadIdx.x < M) inv[o.ptok] = row0 + threadIdx.x;  // read after the barrier below
+      if ((int)threadIdx.x < M) inv[o.ptok] = row0 + threadIdx.x;  // read after the barrier below
     }
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll

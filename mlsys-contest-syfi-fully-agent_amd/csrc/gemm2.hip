@@ -69,8 +69,8 @@ struct S2Regs {
 
 __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
                                         const int32_t* __restrict__ perm_token, const float* __restrict__ perm_w,
-                                        const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
-                                        const float* __restrict__ w2_scale, int n0, int kb0, int lq, int lr) {
+                                        const uint16_t* __restrict__ act, const float* __restrict__ w2_scale, int n0,
+                                        int kb0, int lq, int lr) {
   const int row0 = X.begin(j.e) + j.rt * 16;
   const int rows = min(16, X.end(j.e) - row0);
   // combine operands first: waiting for them never waits for the prefetch
@@ -155,7 +155,7 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
   S2Job j1 = job.e >= 0 ? s2_next(X, active, job) : job;
   S2Regs r0, r1;
   if (job.e >= 0) {
-    s2_load(r0, job, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
+    s2_load(r0, job, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
     s2_copy_w(stage(0), job, w2, n0, kb0, lane);
     s2_copy_w(stage(1), j1.e >= 0 ? j1 : job, w2, n0, kb0, lane);
   }
@@ -178,7 +178,7 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the stage is read: free for the job after next
     const S2Job j2 = j1.e >= 0 ? s2_next(X, active, j1) : j1;
     if (j1.e >= 0) {
-      s2_load(nxt, j1, X, perm_token, perm_w, act, w2, w2_scale, n0, kb0, lq, lr);
+      s2_load(nxt, j1, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
       s2_copy_w(stage(s), j2.e >= 0 ? j2 : j1, w2, n0, kb0, lane);
     }
 #pragma unroll

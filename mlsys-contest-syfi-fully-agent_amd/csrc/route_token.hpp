@@ -5,6 +5,8 @@
 // instead of waiting for a routing launch.
 #pragma once
 
+#include <utility>
+
 #include "moe_common.hpp"
 
 namespace moe {
@@ -168,10 +170,13 @@ struct SmallRoute {
   float pair_w[kSmallRouteMaxTokens][kTopK];       // their weights
   int perm_token[kSmallRouteMaxTokens * kTopK];    // token of each permuted row
   float perm_w[kSmallRouteMaxTokens * kTopK];      // weight of each permuted row
-  // T == 1 (route_one): the token's 32-bit keys, sigmoid scores and group scores
+  // T == 1 (route_one): the token's 32-bit keys, sigmoid scores, group scores,
+  // each group's second largest key, and the compacted top-8 candidates
   uint32_t key1[kEGlobal];
   float s1[kEGlobal];
   float g1[kNGroup];
+  uint32_t gb1[kNGroup];
+  uint64_t cand[16];
 };
 
 struct RouteOut {
@@ -189,6 +194,30 @@ struct RouteOut {
 // only (two keys per lane in wave 0), then the permutation of the single
 // token written directly.  Needs at least 4 waves; ends with a workgroup
 // barrier.
+//
+// The top-8 is a rank, not eight rounds of a wave maximum (one wave's serial
+// chain of ~240 dependent instructions, 1.5 us of the decode layer): each
+// kept group's two largest keys are eight candidates, so the 8th-largest
+// key is at least tau, the least of the kept groups' second largest keys.
+// The keys >= tau (about a dozen) are compacted in expert order into LDS,
+// each lane ranks one of them against all by (key, then lower expert), and
+// the ranks below 8 are the picks, already in ascending expert order.  More
+// than 16 candidates take the eight rounds.
+constexpr int kRankCands = 16;
+
+// 1 where lane (l + K) % 16 of l's DPP row holds a larger 64-bit value than l
+// (row_ror:K), else 0.
+template <int K>
+__device__ __forceinline__ int row_ror_greater(uint32_t lo, uint32_t hi, uint64_t v) {
+  const uint32_t l = (uint32_t)__builtin_amdgcn_mov_dpp((int)lo, 0x120 + K, 0xF, 0xF, true);
+  const uint32_t h = (uint32_t)__builtin_amdgcn_mov_dpp((int)hi, 0x120 + K, 0xF, 0xF, true);
+  return (((uint64_t)h << 32) | l) > v ? 1 : 0;
+}
+template <int... K>
+__device__ __forceinline__ int row_rank_greater(uint32_t lo, uint32_t hi, uint64_t v,
+                                                std::integer_sequence<int, K...>) {
+  return (row_ror_greater<K + 1>(lo, hi, v) + ...);
+}
 __device__ inline void route_one(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf,
                                  int64_t offset, SmallRoute& sr, RouteOut out, bool write_out) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -208,22 +237,23 @@ __device__ inline void route_one(const float* __restrict__ logits, const uint16_
     if (lane == 0) {
       sr.g1[2 * wave] = float_from_order_key(a0) + float_from_order_key(b0);
       sr.g1[2 * wave + 1] = float_from_order_key(a1) + float_from_order_key(b1);
+      sr.gb1[2 * wave] = b0;
+      sr.gb1[2 * wave + 1] = b1;
     }
   }
   __syncthreads();
   if (wave == 0) {
-    // moe.py:139-146: keep the top-4 groups (ties -> lower group index)
-    float G[kNGroup];
+    // moe.py:139-146: keep the top-4 groups (ties -> lower group index);
+    // lane g < 8 ranks group g
+    const int gl = lane & (kNGroup - 1);
+    const float Gl = sr.g1[gl];
+    int grank = 0;
 #pragma unroll
-    for (int g = 0; g < kNGroup; ++g) G[g] = sr.g1[g];
-    uint32_t keep = 0;
-#pragma unroll
-    for (int g = 0; g < kNGroup; ++g) {
-      int rank = 0;
-#pragma unroll
-      for (int h = 0; h < kNGroup; ++h) rank += (G[h] > G[g]) || (G[h] == G[g] && h < g);
-      keep |= (rank < kTopKGroup ? 1u : 0u) << g;
+    for (int h = 0; h < kNGroup; ++h) {
+      const float Gh = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, Gl), h));
+      grank += (Gh > Gl) || (Gh == Gl && h < gl);
     }
+    const uint32_t keep = (uint32_t)__ballot(lane < kNGroup && grank < kTopKGroup) & ((1u << kNGroup) - 1u);
     // Candidates: lane l holds expert 32 kg[l/32] + l%32 (slot 0) and
     // 32 kg[2 + l/32] + l%32 (slot 1), kg the kept groups ascending, so
     // (slot, lane) order is expert order.  Exactly four groups are kept
@@ -243,24 +273,56 @@ __device__ inline void route_one(const float* __restrict__ logits, const uint16_
     int pick[kTopK];
     float wsel[kTopK];
     if (plain) {
-      // moe.py:149-151: eight rounds of (wave maximum, lowest expert holding it)
+      uint32_t tau = ~0u;
 #pragma unroll
-      for (int r = 0; r < kTopK; ++r) {
-        const uint32_t M = wave_max_u32(max(key[0], key[1]));
-        const uint64_t b0 = __ballot(key[0] == M), b1 = __ballot(key[1] == M);
-        const int l = b0 ? __builtin_ctzll(b0) : __builtin_ctzll(b1);
-        const int slot = b0 ? 0 : 1;
-        const int hl = l >> 5;
-        pick[r] = 32 * (slot ? (hl ? kg[3] : kg[2]) : (hl ? kg[1] : kg[0])) + (l & 31);
-        if (lane == l) key[slot] = 0u;  // taken (no candidate key is 0)
-      }
-      constexpr int kNet[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
-                                   {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+      for (int k = 0; k < kTopKGroup; ++k) tau = min(tau, sr.gb1[kg[k]]);
+      const uint64_t c0 = __ballot(key[0] >= tau), c1 = __ballot(key[1] >= tau);
+      const int n0 = __popcll(c0), n = n0 + __popcll(c1);
+      if (n <= kRankCands) {
+        // moe.py:149-151 as a rank: (key, 255 - expert) orders the
+        // candidates as the selection does (larger key first, then the
+        // lower expert); positions follow expert order
+        const uint32_t lo = (uint32_t)c0, hi = (uint32_t)(c0 >> 32);
+        const uint32_t lo1 = (uint32_t)c1, hi1 = (uint32_t)(c1 >> 32);
+        if (key[0] >= tau)
+          sr.cand[__builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0))] =
+              ((uint64_t)key[0] << 32) | (uint32_t)(255 - ea);
+        if (key[1] >= tau)
+          sr.cand[n0 + __builtin_amdgcn_mbcnt_hi(hi1, __builtin_amdgcn_mbcnt_lo(lo1, 0))] =
+              ((uint64_t)key[1] << 32) | (uint32_t)(255 - eb);
+        // lanes 0-15 (one DPP row) hold the candidates, lanes n.. of the row
+        // 0, which ranks below every candidate (keys >= tau > 0)
+        const uint64_t v = lane < n ? sr.cand[lane] : 0;
+        const int rank = row_rank_greater((uint32_t)v, (uint32_t)(v >> 32), v,
+                                          std::make_integer_sequence<int, kRankCands - 1>{});
+        uint64_t sel = __ballot(lane < n && rank < kTopK);  // exactly 8: the ranks are distinct
+        const uint32_t vlo = (uint32_t)v;
 #pragma unroll
-      for (int c = 0; c < 19; ++c) {
-        const int x0 = pick[kNet[c][0]], y0 = pick[kNet[c][1]];
-        pick[kNet[c][0]] = min(x0, y0);
-        pick[kNet[c][1]] = max(x0, y0);
+        for (int r = 0; r < kTopK; ++r) {
+          const int l = __builtin_ctzll(sel);
+          sel &= sel - 1;
+          pick[r] = 255 - (int)(uint32_t)__builtin_amdgcn_readlane((int)vlo, l);
+        }
+      } else {
+        // moe.py:149-151: eight rounds of (wave maximum, lowest expert holding it)
+#pragma unroll
+        for (int r = 0; r < kTopK; ++r) {
+          const uint32_t M = wave_max_u32(max(key[0], key[1]));
+          const uint64_t b0 = __ballot(key[0] == M), b1 = __ballot(key[1] == M);
+          const int l = b0 ? __builtin_ctzll(b0) : __builtin_ctzll(b1);
+          const int slot = b0 ? 0 : 1;
+          const int hl = l >> 5;
+          pick[r] = 32 * (slot ? (hl ? kg[3] : kg[2]) : (hl ? kg[1] : kg[0])) + (l & 31);
+          if (lane == l) key[slot] = 0u;  // taken (no candidate key is 0)
+        }
+        constexpr int kNet[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
+                                     {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+        for (int c = 0; c < 19; ++c) {
+          const int x0 = pick[kNet[c][0]], y0 = pick[kNet[c][1]];
+          pick[kNet[c][0]] = min(x0, y0);
+          pick[kNet[c][1]] = max(x0, y0);
+        }
       }
       // moe.py:154-158: un-biased scores, summed in ascending id order,
       // normalised (true division) then scaled -- as route_token
@@ -270,8 +332,13 @@ __device__ inline void route_one(const float* __restrict__ logits, const uint16_
 #pragma unroll
       for (int k = 0; k < kTopK; ++k) sum = sum + wsel[k];
       const float denom = sum + 1e-20f;
+      // one division per lane (lane r: weight r) instead of eight in a row
+      float mine = wsel[0];
 #pragma unroll
-      for (int k = 0; k < kTopK; ++k) wsel[k] = (wsel[k] / denom) * rsf;
+      for (int r = 1; r < kTopK; ++r) mine = (lane & (kTopK - 1)) == r ? wsel[r] : mine;
+      mine = (mine / denom) * rsf;
+#pragma unroll
+      for (int r = 0; r < kTopK; ++r) wsel[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), r));
     } else {
       route_token(logits, bias, rsf, 0, pick, wsel);
     }

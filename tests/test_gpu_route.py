@@ -110,3 +110,45 @@ def test_exact_ties_go_to_lower_ids(pkg, cuda_device, T):
     assert (ids == torch.arange(8, dtype=torch.int32)).all()
     w = r.topk_w.cpu()
     assert (w == w[0, 0]).all() and abs(float(w[0, 0]) - 2.5 / 8) < 1e-6
+
+
+def test_single_token_routing_matches_per_wave_routing(pkg, cuda_device):
+    """T = 1 routes in a single workgroup with four waves, its top-8 found by
+    a threshold and a rank over the candidates (route_one); T > 16 routes
+    each token on one wave with eight rounds of a wave maximum (route_token).
+    Both restate moe.py:123-158 and must agree bit for bit on the same rows:
+    rows of two synthetic configs (hot experts with a +2 bias among them),
+    rows of a few distinct values (exact ties of keys and of group scores),
+    rows whose top twelve logits are equal (tied candidates of the rank),
+    and all-equal rows (every key ties: more than 16 candidates, which take
+    the eight rounds)."""
+    print("single-token routing against per-wave routing", flush=True)
+    sk = pkg.synth.CONFIGS["skewed_t8192"]
+    pf = pkg.synth.CONFIGS["prefill_t1024"]
+    tok_sk, _ = gpu_tokens(pkg, sk, cuda_device, 384)
+    tok_pf, _ = gpu_tokens(pkg, pf, cuda_device, 256)
+    g = torch.Generator().manual_seed(11)
+    ties = (torch.randint(0, 4, (256, 256), generator=g).float() * 0.25).to(cuda_device)
+    # twelve experts per row share the top logit: about a dozen tied
+    # candidates (the rank, with ties to break by expert)
+    top = torch.randn((128, 256), generator=g) * 0.5
+    for row in top:
+        row[torch.randperm(256, generator=g)[:12]] = 3.0
+    top = top.to(cuda_device)
+    flat = torch.full((4, 256), 0.5, device=cuda_device)
+    for bias in (tok_sk[1], tok_pf[1], torch.zeros_like(tok_pf[1])):
+        logits = torch.cat([tok_sk[0], tok_pf[0], ties, top, flat]).contiguous()
+        n = logits.shape[0]
+        ws = torch.empty_like(pkg.workspace(cuda_device, n))
+        whole = pkg.route(logits, bias, 0, 2.5, ws=ws)
+        ids_all, w_all = whole.topk_ids.clone(), whole.topk_w.clone()
+        ids_one = torch.empty_like(ids_all)
+        w_one = torch.empty_like(w_all)
+        ws1 = torch.empty_like(pkg.workspace(cuda_device, 1))
+        for t in range(n):
+            r = pkg.route(logits[t:t + 1], bias, 0, 2.5, ws=ws1)
+            ids_one[t] = r.topk_ids[0]
+            w_one[t] = r.topk_w[0]
+        torch.cuda.synchronize()
+        bad = (ids_one != ids_all).any(dim=1) | (w_one.view(torch.int32) != w_all.view(torch.int32)).any(dim=1)
+        assert not bad.any(), f"{int(bad.sum())} of {n} rows differ, first {int(bad.nonzero()[0])}"
