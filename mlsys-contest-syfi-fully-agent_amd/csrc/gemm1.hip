@@ -164,8 +164,19 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     o.s0 = hs_scale[(size_t)(kb0 + (lane >> 4)) * T + tok];
     o.s1 = x1 < kS1KB * 16 ? hs_scale[(size_t)(kb0 + (x1 >> 4)) * T + tok] : 0.f;
     const uint8_t* ap = hs + (size_t)tok * kH + kb0 * kBlk + 32 * lq;
+    if (kDirect) {
+      // only the lanes of real rows load (rows >= T are discarded): at
+      // T = 1 the other 15 rows' lanes would fetch the same token again
 #pragma unroll
-    for (int j = 0; j < kS1KB; ++j) o.a[j] = *(const v8i*)(ap + j * kBlk);
+      for (int j = 0; j < kS1KB; ++j) o.a[j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+      if (lr < rows) {
+#pragma unroll
+        for (int j = 0; j < kS1KB; ++j) o.a[j] = *(const v8i*)(ap + j * kBlk);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kS1KB; ++j) o.a[j] = *(const v8i*)(ap + j * kBlk);
+    }
   };
   // kDirect: the expert's permutation entries (LDS), the only per-expert
   // part of the row operands
@@ -270,6 +281,11 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     copy_w(i0, 0);
     copy_w(i0, 1);
     issue_sw(i0, cur);
+    // kDirect: the token rows land while the copies are issued.  Left
+    // pending into the item loop (which loads no register of its own), they
+    // made the compiler wait for every outstanding load before the loop,
+    // the first item's whole weight copy included.
+    if (kDirect) wait_vmcnt<kS1CopyOps0 + kS1CopyOps1>();
   }
   // fragment of block j: lane (q, r) holds row r, K bytes 32q .. 32q+31
   const int slot_lo = wide_slot(lr, 2 * lq), slot_hi = wide_slot(lr, 2 * lq + 1);

@@ -252,6 +252,14 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
 }
 
+// s_waitcnt vmcnt(N) alone (lgkmcnt left at its maximum): scalar and LDS
+// loads may stay in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Waits until at most `ahead` pipeline stages of `per_stage` vector-memory
 // operations each are still in flight (ahead = 0, 1, 2, 3).
 template <int per_stage>

@@ -205,6 +205,11 @@ struct RouteOut {
 // than 16 candidates take the eight rounds.
 constexpr int kRankCands = 16;
 
+// Set bits of a wave mask below this lane (mbcnt).
+__device__ __forceinline__ int lane_rank(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 // 1 where lane (l + K) % 16 of l's DPP row holds a larger 64-bit value than l
 // (row_ror:K), else 0.
 template <int K>
@@ -247,6 +252,7 @@ __device__ inline void route_one(const float* __restrict__ logits, const uint16_
     // lane g < 8 ranks group g
     const int gl = lane & (kNGroup - 1);
     const float Gl = sr.g1[gl];
+    const uint32_t gbl = sr.gb1[gl];
     int grank = 0;
 #pragma unroll
     for (int h = 0; h < kNGroup; ++h) {
@@ -270,40 +276,41 @@ __device__ inline void route_one(const float* __restrict__ logits, const uint16_
     const int ea = 32 * (half ? kg[1] : kg[0]) + (lane & 31), eb = 32 * (half ? kg[3] : kg[2]) + (lane & 31);
     uint32_t key[2] = {sr.key1[ea], sr.key1[eb]};
     const bool plain = __popc(keep) == kTopKGroup && !__ballot(key[0] == 0u || key[1] == 0u);
-    int pick[kTopK];
-    float wsel[kTopK];
+    // pick_l: lane r < 8 receives the r-th pick (ascending expert id)
+    int pick_l = 0;
+    bool ranked = false;
     if (plain) {
-      uint32_t tau = ~0u;
-#pragma unroll
-      for (int k = 0; k < kTopKGroup; ++k) tau = min(tau, sr.gb1[kg[k]]);
+      // tau: minimum over lanes 0-7 (row 0's first half) of the kept
+      // groups' second largest keys
+      uint32_t t = (keep >> gl) & 1u ? gbl : ~0u;
+      t = min(t, dpp_u32<kDppQuad1032, 0xF>(t));
+      t = min(t, dpp_u32<kDppQuad2301, 0xF>(t));
+      t = min(t, dpp_u32<kDppRowHalfMirror, 0xF>(t));
+      const uint32_t tau = (uint32_t)__builtin_amdgcn_readlane((int)t, 0);
       const uint64_t c0 = __ballot(key[0] >= tau), c1 = __ballot(key[1] >= tau);
       const int n0 = __popcll(c0), n = n0 + __popcll(c1);
       if (n <= kRankCands) {
         // moe.py:149-151 as a rank: (key, 255 - expert) orders the
         // candidates as the selection does (larger key first, then the
         // lower expert); positions follow expert order
-        const uint32_t lo = (uint32_t)c0, hi = (uint32_t)(c0 >> 32);
-        const uint32_t lo1 = (uint32_t)c1, hi1 = (uint32_t)(c1 >> 32);
-        if (key[0] >= tau)
-          sr.cand[__builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0))] =
-              ((uint64_t)key[0] << 32) | (uint32_t)(255 - ea);
-        if (key[1] >= tau)
-          sr.cand[n0 + __builtin_amdgcn_mbcnt_hi(hi1, __builtin_amdgcn_mbcnt_lo(lo1, 0))] =
-              ((uint64_t)key[1] << 32) | (uint32_t)(255 - eb);
+        if (key[0] >= tau) sr.cand[lane_rank(c0)] = ((uint64_t)key[0] << 32) | (uint32_t)(255 - ea);
+        if (key[1] >= tau) sr.cand[n0 + lane_rank(c1)] = ((uint64_t)key[1] << 32) | (uint32_t)(255 - eb);
         // lanes 0-15 (one DPP row) hold the candidates, lanes n.. of the row
         // 0, which ranks below every candidate (keys >= tau > 0)
         const uint64_t v = lane < n ? sr.cand[lane] : 0;
         const int rank = row_rank_greater((uint32_t)v, (uint32_t)(v >> 32), v,
                                           std::make_integer_sequence<int, kRankCands - 1>{});
-        uint64_t sel = __ballot(lane < n && rank < kTopK);  // exactly 8: the ranks are distinct
-        const uint32_t vlo = (uint32_t)v;
-#pragma unroll
-        for (int r = 0; r < kTopK; ++r) {
-          const int l = __builtin_ctzll(sel);
-          sel &= sel - 1;
-          pick[r] = 255 - (int)(uint32_t)__builtin_amdgcn_readlane((int)vlo, l);
-        }
-      } else {
+        const bool chosen = lane < n && rank < kTopK;
+        const uint64_t selm = __ballot(chosen);  // exactly 8: the ranks are distinct
+        // a chosen candidate goes to the lane of its place in expert order
+        // (the others to lane 63, which is never read)
+        pick_l = __builtin_amdgcn_ds_permute((chosen ? lane_rank(selm) : kWave - 1) * 4, 255 - (int)(uint32_t)v);
+        ranked = true;
+      }
+    }
+    if (!ranked) {
+      int pick[kTopK];
+      if (plain) {
         // moe.py:149-151: eight rounds of (wave maximum, lowest expert holding it)
 #pragma unroll
         for (int r = 0; r < kTopK; ++r) {
@@ -323,70 +330,50 @@ __device__ inline void route_one(const float* __restrict__ logits, const uint16_
           pick[kNet[c][0]] = min(x0, y0);
           pick[kNet[c][1]] = max(x0, y0);
         }
+      } else {
+        float wsel[kTopK];  // the same weights as computed below (same scores, same order)
+        route_token(logits, bias, rsf, 0, pick, wsel);
       }
-      // moe.py:154-158: un-biased scores, summed in ascending id order,
-      // normalised (true division) then scaled -- as route_token
 #pragma unroll
-      for (int r = 0; r < kTopK; ++r) wsel[r] = sr.s1[pick[r]];
-      float sum = 0.0f;
-#pragma unroll
-      for (int k = 0; k < kTopK; ++k) sum = sum + wsel[k];
-      const float denom = sum + 1e-20f;
-      // one division per lane (lane r: weight r) instead of eight in a row
-      float mine = wsel[0];
-#pragma unroll
-      for (int r = 1; r < kTopK; ++r) mine = (lane & (kTopK - 1)) == r ? wsel[r] : mine;
-      mine = (mine / denom) * rsf;
-#pragma unroll
-      for (int r = 0; r < kTopK; ++r) wsel[r] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), r));
-    } else {
-      route_token(logits, bias, rsf, 0, pick, wsel);
+      for (int r = 0; r < kTopK; ++r) pick_l = (lane & (kTopK - 1)) == r ? pick[r] : pick_l;
     }
+    pick_l &= kEGlobal - 1;  // lanes past 8 hold no pick
+    // moe.py:154-158: un-biased scores, summed in ascending id order,
+    // normalised (true division) then scaled -- as route_token; lane r
+    // divides weight r
+    const float s_l = sr.s1[pick_l];
+    float sum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kTopK; ++r) sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s_l), r));
+    const float w_l = (s_l / (sum + 1e-20f)) * rsf;
     // moe.py:168-179 for one token: its local experts, ascending, take rows
     // 0, 1, ...; expert_off[le] counts the local picks below le
-    int row_of[kTopK];
-    int rows = 0;
+    const int64_t le = (int64_t)pick_l - offset;
+    const bool loc = lane < kTopK && le >= 0 && le < kELocal;
+    const int row = loc ? lane_rank(__ballot(loc)) : -1;
+    uint32_t lm = 0u;  // bit le: local expert le is picked
 #pragma unroll
-    for (int r = 0; r < kTopK; ++r) {
-      const int64_t le = (int64_t)pick[r] - offset;
-      row_of[r] = (le >= 0 && le < kELocal) ? rows++ : -1;
-    }
+    for (int r = 0; r < kTopK; ++r) lm |= (uint32_t)__builtin_amdgcn_readlane(loc ? (int)(1u << (int)le) : 0, r);
     if (lane <= kELocal) {
-      int below = 0;
-      uint32_t mine = 0u;
-#pragma unroll
-      for (int r = 0; r < kTopK; ++r) {
-        const int64_t le = (int64_t)pick[r] - offset;
-        if (row_of[r] >= 0 && le < lane) ++below;
-        if (row_of[r] >= 0 && le == lane) mine = 1u;
-      }
+      const int below = __popc((uint32_t)((uint64_t)lm & ((1ull << lane) - 1ull)));
       sr.expert_off[lane] = below;
       if (write_out) out.expert_off[lane] = below;
-      if (lane < kELocal) sr.tokmask[lane] = mine;
+      if (lane < kELocal) sr.tokmask[lane] = (lm >> lane) & 1u;
     }
     if (lane < kTopK) {
-      int e = pick[0], row = row_of[0];
-      float we = wsel[0];
-#pragma unroll
-      for (int r = 1; r < kTopK; ++r)
-        if (lane == r) {
-          e = pick[r];
-          row = row_of[r];
-          we = wsel[r];
-        }
-      sr.pair_id[0][lane] = e;
-      sr.pair_w[0][lane] = we;
+      sr.pair_id[0][lane] = pick_l;
+      sr.pair_w[0][lane] = w_l;
       if (row >= 0) {
         sr.perm_token[row] = 0;
-        sr.perm_w[row] = we;
+        sr.perm_w[row] = w_l;
       }
       if (write_out) {
-        out.ids[lane] = e;
-        out.w[lane] = we;
+        out.ids[lane] = pick_l;
+        out.w[lane] = w_l;
         out.pair_row[lane] = row;
         if (row >= 0) {
           out.perm_token[row] = 0;
-          out.perm_w[row] = we;
+          out.perm_w[row] = w_l;
         }
       }
     }
