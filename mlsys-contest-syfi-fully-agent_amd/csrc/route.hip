@@ -81,11 +81,30 @@ __device__ __forceinline__ void expert_offsets(PermShared& sh, bool write_off, i
   }
 }
 
+// A token's ids and weights, loaded at the start of the permutation pass so
+// that their latency overlaps the histogram reduction's.
+struct TokenPicks {
+  int4 a, b;    // ids
+  float4 u, v;  // weights
+};
+// Lanes past the last token load its row again (unused): a load under a
+// branch would make the compiler wait for it where the branch rejoins.
+__device__ __forceinline__ TokenPicks load_picks(const int32_t* __restrict__ ids, const float* __restrict__ topk_w,
+                                                 int T, int t) {
+  const size_t tc = (size_t)min(t, T - 1);
+  TokenPicks p;
+  p.a = *(const int4*)(ids + tc * kTopK);
+  p.b = *(const int4*)(ids + tc * kTopK + 4);
+  p.u = *(const float4*)(topk_w + tc * kTopK);
+  p.v = *(const float4*)(topk_w + tc * kTopK + 4);
+  return p;
+}
+
 // Rows of the pairs of tokens [t0, t0 + 1024): ascending token order inside
 // each expert, starting at sh.running[e].  All 1024 threads take part.
-__device__ void scatter_chunk(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int T, int t0,
-                              int64_t offset, PermShared& sh, int32_t* __restrict__ pair_row,
-                              int32_t* __restrict__ perm_token, float* __restrict__ perm_w) {
+__device__ void scatter_chunk(const TokenPicks& pk, int T, int t0, int64_t offset, PermShared& sh,
+                              int32_t* __restrict__ pair_row, int32_t* __restrict__ perm_token,
+                              float* __restrict__ perm_w) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -93,9 +112,7 @@ __device__ void scatter_chunk(const int32_t* __restrict__ ids, const float* __re
   int kf = kTopK;
   uint32_t m = 0;  // tokens past T have no local expert
   if (t < T) {
-    const int4 a = *(const int4*)(ids + (size_t)t * kTopK);
-    const int4 b = *(const int4*)(ids + (size_t)t * kTopK + 4);
-    const int32_t id[kTopK] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const int32_t id[kTopK] = {pk.a.x, pk.a.y, pk.a.z, pk.a.w, pk.b.x, pk.b.y, pk.b.z, pk.b.w};
     m = local_mask(id, offset, kf);
   }
   // per-expert counts of this wave: lane le keeps popc(ballot of expert le)
@@ -137,11 +154,12 @@ __device__ void scatter_chunk(const int32_t* __restrict__ ids, const float* __re
     r1.x = row[4]; r1.y = row[5]; r1.z = row[6]; r1.w = row[7];
     *(int4*)(pair_row + (size_t)t * kTopK) = r0;
     *(int4*)(pair_row + (size_t)t * kTopK + 4) = r1;
+    const float wv[kTopK] = {pk.u.x, pk.u.y, pk.u.z, pk.u.w, pk.v.x, pk.v.y, pk.v.z, pk.v.w};
 #pragma unroll
     for (int k = 0; k < kTopK; ++k)
       if (row[k] >= 0) {
         perm_token[row[k]] = t;
-        perm_w[row[k]] = topk_w[(size_t)t * kTopK + k];
+        perm_w[row[k]] = wv[k];
       }
   }
   __syncthreads();  // wave_cnt / wave_base may be reused
@@ -212,16 +230,35 @@ perm_kernel(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, i
   __shared__ int part_pre[kGroups][kELocal];
   const int nb = (T + tokens_per_block - 1) / tokens_per_block;
   const int first = blockIdx.x * (kRouteThreads / tokens_per_block);  // route workgroups before this chunk
+  const TokenPicks pk0 = load_picks(ids, topk_w, T, blockIdx.x * kRouteThreads + threadIdx.x);
   const int e = threadIdx.x % kELocal;
   const int g = threadIdx.x / kELocal;
   int tot = 0, pre = 0;
-  for (int b = g; b < nb; b += kGroups) {
-    const int v = block_hist[(size_t)b * kELocal + e];
-    tot += v;
-    if (b < first) pre += v;
+  // eight histogram loads in flight per thread (one wait per batch, not per
+  // load: T = 1024 has 256 route histograms, 8 per thread), from clamped
+  // addresses so that no load sits under a branch
+  constexpr int kBatch = 8;
+  for (int b0 = g; b0 < nb; b0 += kBatch * kGroups) {
+    int v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) v[i] = block_hist[(size_t)min(b0 + i * kGroups, nb - 1) * kELocal + e];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int b = b0 + i * kGroups;
+      const int x = b < nb ? v[i] : 0;
+      tot += x;
+      if (b < first) pre += x;
+    }
   }
   part_tot[g][e] = tot;
   part_pre[g][e] = pre;
+  // the picks are first used only here, after the histogram loads went out
+  // (the compiler would otherwise use them first and wait for them alone)
+  TokenPicks pk = pk0;
+  asm volatile("" : "+v"(pk.a.x), "+v"(pk.a.y), "+v"(pk.a.z), "+v"(pk.a.w), "+v"(pk.b.x), "+v"(pk.b.y),
+               "+v"(pk.b.z), "+v"(pk.b.w)::"memory");
+  asm volatile("" : "+v"(pk.u.x), "+v"(pk.u.y), "+v"(pk.u.z), "+v"(pk.u.w), "+v"(pk.v.x), "+v"(pk.v.y),
+               "+v"(pk.v.z), "+v"(pk.v.w)::"memory");
   __syncthreads();
   if (threadIdx.x < kELocal) {
     int a = 0, p = 0;
@@ -236,7 +273,7 @@ perm_kernel(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, i
   __syncthreads();
   if (threadIdx.x < kWave) expert_offsets(sh, blockIdx.x == 0, expert_off);
   __syncthreads();
-  scatter_chunk(ids, topk_w, T, blockIdx.x * kRouteThreads, offset, sh, pair_row, perm_token, perm_w);
+  scatter_chunk(pk, T, blockIdx.x * kRouteThreads, offset, sh, pair_row, perm_token, perm_w);
 }
 
 }  // namespace
