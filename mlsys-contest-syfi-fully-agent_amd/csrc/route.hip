@@ -11,9 +11,10 @@
 //     owns experts l, l+64, l+128, l+192, so a routing group of 32 experts is
 //     one half-wave in one register slot;
 //   * scores become 32-bit order-preserving keys; the group top-2 sums use
-//     one DPP top-2 reduction per half-wave (four slots in parallel), and the
-//     top-8 is eight rounds of a DPP wave maximum plus ballots for the lowest
-//     expert holding it, the ids then sorted by a comparator network;
+//     one DPP top-2 reduction per half-wave (four slots in parallel), the
+//     groups are ranked one per lane, and the top-8 is a rank of the few
+//     candidates at or above the kept groups' least second-largest key (DPP
+//     row rotations), in expert order (route_token_lanes);
 //   * T <= 16 (decode): the single workgroup also builds the permutation from
 //     LDS (per-expert token bitmasks), with no global atomics, fences or
 //     re-reads of the ids (route_small, route_token.hpp).  The layer itself
@@ -188,6 +189,8 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
     return;
   }
   __shared__ int hist[kELocal];
+  __shared__ uint64_t cand[kW][kRankCands];  // per wave: the top-8 candidates
+  __shared__ float cand_s[kW][kRankCands];
   if (threadIdx.x < kELocal) hist[threadIdx.x] = 0;
   __syncthreads();
 
@@ -195,18 +198,10 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
   const int tw = threadIdx.x / kWave;
   const int t = blockIdx.x * kW + tw;
   if (t < T) {
-    int sel[kTopK];
-    float wsel[kTopK];
-    route_token(logits, bias, rsf, t, sel, wsel);
+    int e;
+    float we;
+    route_token_lanes(logits, bias, rsf, t, cand[tw], cand_s[tw], e, we);
     if (lane < kTopK) {
-      int e = sel[0];
-      float we = wsel[0];
-#pragma unroll
-      for (int r = 1; r < kTopK; ++r)
-        if (lane == r) {
-          e = sel[r];
-          we = wsel[r];
-        }
       ids[(size_t)t * kTopK + lane] = e;
       w[(size_t)t * kTopK + lane] = we;
       const int64_t le = (int64_t)e - offset;

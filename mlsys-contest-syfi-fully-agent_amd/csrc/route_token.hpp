@@ -48,59 +48,15 @@ __device__ __forceinline__ void halfwave_top2(uint32_t k, uint32_t& a0, uint32_t
   b1 = (uint32_t)__builtin_amdgcn_readlane((int)b, 63);
 }
 
-// Routes token t with one wavefront.  Returns the 8 selected ids, ascending
-// (wave-uniform), and their weights (wave-uniform).
-//
-// Lane l holds experts l, l+64, l+128, l+192 (slot j = expert / 64); the
-// routing group of 32 experts g = 2j + (l >= 32) is one half-wave of one slot.
-// Scores are compared through 32-bit order-preserving keys of the fp32 values
-// (masked experts: key 0, below every real score); among equal scores the
-// lower expert index wins.
-__device__ inline void route_token(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
-                            float rsf, int t, int sel[kTopK], float wsel[kTopK]) {
+// moe.py:149-151: top-8 experts among the kept groups, as eight rounds of
+// (wave maximum of the keys, the lowest expert index holding it); the expert
+// taken leaves the round's candidates.  This is the set "every key above the
+// 8th largest, then the lowest indices among the keys equal to it" (keys of
+// dropped groups must be 0, below every real score).  Lane l holds experts
+// 64 j + l in slot j; the picks come out ascending.
+__device__ __forceinline__ void top8_rounds(uint32_t key[4], int pick[kTopK]) {
   const int lane = threadIdx.x & (kWave - 1);
-  float s[4];
-  uint32_t key[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = 64 * j + lane;
-    const float x = logits[(size_t)t * kEGlobal + e];
-    // moe.py:127: s = 1/(1+exp(-x)); exp evaluated in double, rounded once.
-    const float ex = (float)exp(-(double)x);
-    s[j] = 1.0f / (1.0f + ex);
-    // moe.py:128: s_with_bias = s + bias
-    key[j] = float_order_key(s[j] + bf16_to_f32(bias[e]));
-  }
-  // moe.py:135-136: group score = sum of the two largest biased scores (a
-  // repeated maximum counts twice).  The four slots reduce independently.
-  float G[kNGroup];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t a0, b0, a1, b1;
-    halfwave_top2(key[j], a0, b0, a1, b1);
-    G[2 * j] = float_from_order_key(a0) + float_from_order_key(b0);
-    G[2 * j + 1] = float_from_order_key(a1) + float_from_order_key(b1);
-  }
-  // moe.py:139-146: keep the top-4 groups (ties -> lower group index).
-  uint32_t keep = 0;
-#pragma unroll
-  for (int g = 0; g < kNGroup; ++g) {
-    int rank = 0;
-#pragma unroll
-    for (int h = 0; h < kNGroup; ++h) rank += (G[h] > G[g]) || (G[h] == G[g] && h < g);
-    keep |= (rank < kTopKGroup ? 1u : 0u) << g;
-  }
-  // moe.py:149-151: top-8 experts among the kept groups, as eight rounds of
-  // (wave maximum of the keys, the lowest expert index holding it); the
-  // expert taken leaves the round's candidates.  This is the set "every key
-  // above the 8th largest, then the lowest indices among the keys equal to
-  // it" (keys of dropped groups are 0, below every real score).
-  const int half = lane >> 5;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (!((keep >> (2 * j + half)) & 1u)) key[j] = 0u;
   uint32_t taken = 0u;  // bit j: this lane's expert 64j + lane already taken
-  int pick[kTopK];
 #pragma unroll
   for (int r = 0; r < kTopK; ++r) {
     const uint32_t M = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
@@ -136,6 +92,69 @@ __device__ inline void route_token(const float* __restrict__ logits, const uint1
     pick[kNet[c][0]] = min(x, y);
     pick[kNet[c][1]] = max(x, y);
   }
+}
+
+// moe.py:127-136 for token t on one wave: the un-biased scores s, the 32-bit
+// keys of the biased scores, and per group the top-2 sum and the second
+// largest key.
+__device__ __forceinline__ void token_keys(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
+                                           int t, float s[4], uint32_t key[4], float G[kNGroup],
+                                           uint32_t gb[kNGroup]) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 64 * j + lane;
+    const float x = logits[(size_t)t * kEGlobal + e];
+    // moe.py:127: s = 1/(1+exp(-x)); exp evaluated in double, rounded once.
+    const float ex = (float)exp(-(double)x);
+    s[j] = 1.0f / (1.0f + ex);
+    // moe.py:128: s_with_bias = s + bias
+    key[j] = float_order_key(s[j] + bf16_to_f32(bias[e]));
+  }
+  // moe.py:135-136: group score = sum of the two largest biased scores (a
+  // repeated maximum counts twice).  The four slots reduce independently.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t a0, b0, a1, b1;
+    halfwave_top2(key[j], a0, b0, a1, b1);
+    G[2 * j] = float_from_order_key(a0) + float_from_order_key(b0);
+    G[2 * j + 1] = float_from_order_key(a1) + float_from_order_key(b1);
+    gb[2 * j] = b0;
+    gb[2 * j + 1] = b1;
+  }
+}
+
+// Routes token t with one wavefront.  Returns the 8 selected ids, ascending
+// (wave-uniform), and their weights (wave-uniform).
+//
+// Lane l holds experts l, l+64, l+128, l+192 (slot j = expert / 64); the
+// routing group of 32 experts g = 2j + (l >= 32) is one half-wave of one slot.
+// Scores are compared through 32-bit order-preserving keys of the fp32 values
+// (masked experts: key 0, below every real score); among equal scores the
+// lower expert index wins.
+__device__ inline void route_token(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
+                            float rsf, int t, int sel[kTopK], float wsel[kTopK]) {
+  const int lane = threadIdx.x & (kWave - 1);
+  float s[4];
+  uint32_t key[4];
+  float G[kNGroup];
+  uint32_t gb[kNGroup];
+  token_keys(logits, bias, t, s, key, G, gb);
+  // moe.py:139-146: keep the top-4 groups (ties -> lower group index).
+  uint32_t keep = 0;
+#pragma unroll
+  for (int g = 0; g < kNGroup; ++g) {
+    int rank = 0;
+#pragma unroll
+    for (int h = 0; h < kNGroup; ++h) rank += (G[h] > G[g]) || (G[h] == G[g] && h < g);
+    keep |= (rank < kTopKGroup ? 1u : 0u) << g;
+  }
+  const int half = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (!((keep >> (2 * j + half)) & 1u)) key[j] = 0u;
+  int pick[kTopK];
+  top8_rounds(key, pick);
 #pragma unroll
   for (int r = 0; r < kTopK; ++r) {
     const int j = pick[r] >> 6, l = pick[r] & 63;
@@ -177,6 +196,9 @@ struct SmallRoute {
   float g1[kNGroup];
   uint32_t gb1[kNGroup];
   uint64_t cand[16];
+  // T >= 2 (route_token_lanes, a wave per token): each wave's top-8 candidates
+  uint64_t cand_w[kSmallRouteMaxTokens][16];
+  float cand_sw[kSmallRouteMaxTokens][16];
 };
 
 struct RouteOut {
@@ -188,22 +210,16 @@ struct RouteOut {
   float* perm_w;
 };
 
-// T == 1: the same routing as route_token, with the work of one token spread
-// over four waves (waves 0-3 each compute one 64-expert slot's keys and its
-// two group scores) and the top-8 over the 128 experts of the kept groups
-// only (two keys per lane in wave 0), then the permutation of the single
-// token written directly.  Needs at least 4 waves; ends with a workgroup
-// barrier.
-//
-// The top-8 is a rank, not eight rounds of a wave maximum (one wave's serial
-// chain of ~240 dependent instructions, 1.5 us of the decode layer): each
-// kept group's two largest keys are eight candidates, so the 8th-largest
-// key is at least tau, the least of the kept groups' second largest keys.
-// The keys >= tau (about a dozen) are compacted in expert order into LDS,
-// each lane ranks one of them against all by (key, then lower expert), and
-// the ranks below 8 are the picks, already in ascending expert order.  More
-// than 16 candidates take the eight rounds.
+// The top-8 as a rank rather than eight rounds of a wave maximum (one wave's
+// serial chain of ~240 dependent instructions, 1.5 us of the decode layer):
+// each kept group's two largest keys are eight candidates, so the
+// 8th-largest key is at least tau, the least of the kept groups' second
+// largest keys.  The keys >= tau (about a dozen) are compacted in expert
+// order into LDS, each lane ranks one of them against all by (key, then
+// lower expert), and the ranks below 8 are the picks, already in ascending
+// expert order.  More than kRankCands candidates take the eight rounds.
 constexpr int kRankCands = 16;
+static_assert(kRankCands == 16, "one DPP row of candidates; SmallRoute sizes its scratch for 16");
 
 // Set bits of a wave mask below this lane (mbcnt).
 __device__ __forceinline__ int lane_rank(uint64_t m) {
@@ -223,6 +239,114 @@ __device__ __forceinline__ int row_rank_greater(uint32_t lo, uint32_t hi, uint64
                                                 std::integer_sequence<int, K...>) {
   return (row_ror_greater<K + 1>(lo, hi, v) + ...);
 }
+
+// route_token with the result per lane (lane r < 8: pick r, ascending, and
+// its weight) and the top-8 found as route_one does: the groups are ranked
+// one per lane, the kept groups' keys at or above tau (the least of their
+// second largest keys) are compacted in expert order into `cand` / `cs`
+// (16 entries of this wave's LDS) and ranked against each other by DPP row
+// rotations, and each of lanes 0-7 divides its own weight.  More than 16
+// candidates, fewer than four kept groups (NaN scores) or a kept key of 0
+// take the eight rounds.  Same results as route_token, bit for bit.
+__device__ inline void route_token_lanes(const float* __restrict__ logits, const uint16_t* __restrict__ bias,
+                                         float rsf, int t, uint64_t* cand, float* cs, int& pick_l, float& w_l) {
+  const int lane = threadIdx.x & (kWave - 1);
+  float s[4];
+  uint32_t key[4];
+  float G[kNGroup];
+  uint32_t gb[kNGroup];
+  token_keys(logits, bias, t, s, key, G, gb);
+  // moe.py:139-146: keep the top-4 groups (ties -> lower group index);
+  // lane g < 8 ranks group g
+  const int gl = lane & (kNGroup - 1);
+  float Gl = G[0];
+  uint32_t gbl = gb[0];
+#pragma unroll
+  for (int g = 1; g < kNGroup; ++g) {
+    Gl = gl == g ? G[g] : Gl;
+    gbl = gl == g ? gb[g] : gbl;
+  }
+  int grank = 0;
+#pragma unroll
+  for (int h = 0; h < kNGroup; ++h) grank += (G[h] > Gl) || (G[h] == Gl && h < gl);
+  const uint32_t keep = (uint32_t)__ballot(lane < kNGroup && grank < kTopKGroup) & ((1u << kNGroup) - 1u);
+  const int half = lane >> 5;
+  bool kept[4], zero = false;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    kept[j] = (keep >> (2 * j + half)) & 1u;
+    zero |= kept[j] && key[j] == 0u;
+  }
+  float s_l = 0.0f;
+  bool ranked = false;
+  if (__popc(keep) == kTopKGroup && !__ballot(zero)) {
+    uint32_t tm = (keep >> gl) & 1u ? gbl : ~0u;
+    tm = min(tm, dpp_u32<kDppQuad1032, 0xF>(tm));
+    tm = min(tm, dpp_u32<kDppQuad2301, 0xF>(tm));
+    tm = min(tm, dpp_u32<kDppRowHalfMirror, 0xF>(tm));
+    const uint32_t tau = (uint32_t)__builtin_amdgcn_readlane((int)tm, 0);
+    uint64_t c[4];
+    int base[5];
+    base[0] = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = __ballot(kept[j] && key[j] >= tau);
+      base[j + 1] = base[j] + __popcll(c[j]);
+    }
+    const int n = base[4];
+    if (n <= kRankCands) {
+      // moe.py:149-151 as a rank over (key, 255 - expert), positions in
+      // expert order (slot-major, then lane)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (kept[j] && key[j] >= tau) {
+          const int pos = base[j] + lane_rank(c[j]);
+          cand[pos] = ((uint64_t)key[j] << 32) | (uint32_t)(255 - (64 * j + lane));
+          cs[pos] = s[j];
+        }
+      const uint64_t v = lane < n ? cand[lane] : 0;
+      const float sv = lane < n ? cs[lane] : 0.0f;
+      const int rank = row_rank_greater((uint32_t)v, (uint32_t)(v >> 32), v,
+                                        std::make_integer_sequence<int, kRankCands - 1>{});
+      const bool chosen = lane < n && rank < kTopK;
+      const int dst = (chosen ? lane_rank(__ballot(chosen)) : kWave - 1) * 4;
+      pick_l = __builtin_amdgcn_ds_permute(dst, 255 - (int)(uint32_t)v);
+      s_l = __builtin_bit_cast(float, __builtin_amdgcn_ds_permute(dst, __builtin_bit_cast(int, sv)));
+      ranked = true;
+    }
+  }
+  if (!ranked) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (!kept[j]) key[j] = 0u;
+    int pick[kTopK];
+    top8_rounds(key, pick);
+    pick_l = pick[0];
+#pragma unroll
+    for (int r = 0; r < kTopK; ++r) {
+      const int j = pick[r] >> 6, l = pick[r] & 63;
+      const float sj = j == 0 ? s[0] : j == 1 ? s[1] : j == 2 ? s[2] : s[3];
+      const float sr_ = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sj), l));
+      if (gl == r) {
+        pick_l = pick[r];
+        s_l = sr_;
+      }
+    }
+  }
+  // moe.py:154-158: un-biased scores summed in ascending id order,
+  // normalised (true division) then scaled; lane r divides weight r
+  float sum = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kTopK; ++r) sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s_l), r));
+  w_l = (s_l / (sum + 1e-20f)) * rsf;
+}
+
+// T == 1: the same routing as route_token, with the work of one token spread
+// over four waves (waves 0-3 each compute one 64-expert slot's keys and its
+// two group scores) and the top-8 (as a rank, above) over the 128 experts of
+// the kept groups only (two keys per lane in wave 0), then the permutation
+// of the single token written directly.  Needs at least 4 waves; ends with
+// a workgroup barrier.
 __device__ inline void route_one(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf,
                                  int64_t offset, SmallRoute& sr, RouteOut out, bool write_out) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -393,18 +517,10 @@ __device__ inline void route_small(const float* __restrict__ logits, const uint1
   if (threadIdx.x < kELocal) sr.tokmask[threadIdx.x] = 0u;
   __syncthreads();
   for (int t = wave; t < T; t += waves) {
-    int sel[kTopK];
-    float wsel[kTopK];
-    route_token(logits, bias, rsf, t, sel, wsel);
+    int e;
+    float we;
+    route_token_lanes(logits, bias, rsf, t, sr.cand_w[wave], sr.cand_sw[wave], e, we);
     if (lane < kTopK) {
-      int e = sel[0];
-      float we = wsel[0];
-#pragma unroll
-      for (int r = 1; r < kTopK; ++r)
-        if (lane == r) {
-          e = sel[r];
-          we = wsel[r];
-        }
       if (write_out) {
         out.ids[(size_t)t * kTopK + lane] = e;
         out.w[(size_t)t * kTopK + lane] = we;
