@@ -53,10 +53,11 @@ __device__ __forceinline__ uint32_t local_mask(const int32_t id[kTopK], int64_t 
   return m;
 }
 
-// Shared memory of the permutation pass.
+// Shared memory of the permutation pass, for a workgroup of kPW waves.
+template <int kPW>
 struct PermShared {
-  int wave_cnt[kRouteWaves][kELocal];
-  int wave_base[kRouteWaves][kELocal];
+  int wave_cnt[kPW][kELocal];
+  int wave_base[kPW][kELocal];
   int running[kELocal];  // next free row per expert
   int total[kELocal];    // pairs per expert (all tokens)
   int before[kELocal];   // pairs per expert in tokens before this chunk
@@ -64,7 +65,8 @@ struct PermShared {
 
 // Writes expert_off (when `write_off`) and sets running[e] = expert_off[e] +
 // before[e] from the totals in shared memory.  Called by wave 0.
-__device__ __forceinline__ void expert_offsets(PermShared& sh, bool write_off, int32_t* __restrict__ expert_off) {
+template <int kPW>
+__device__ __forceinline__ void expert_offsets(PermShared<kPW>& sh, bool write_off, int32_t* __restrict__ expert_off) {
   const int lane = threadIdx.x & (kWave - 1);
   const int c = lane < kELocal ? sh.total[lane] : 0;
   int incl = c;
@@ -101,9 +103,10 @@ __device__ __forceinline__ TokenPicks load_picks(const int32_t* __restrict__ ids
   return p;
 }
 
-// Rows of the pairs of tokens [t0, t0 + 1024): ascending token order inside
-// each expert, starting at sh.running[e].  All 1024 threads take part.
-__device__ void scatter_chunk(const TokenPicks& pk, int T, int t0, int64_t offset, PermShared& sh,
+// Rows of the pairs of tokens [t0, t0 + 64 kPW): ascending token order inside
+// each expert, starting at sh.running[e].  Every thread takes part.
+template <int kPW>
+__device__ void scatter_chunk(const TokenPicks& pk, int T, int t0, int64_t offset, PermShared<kPW>& sh,
                               int32_t* __restrict__ pair_row, int32_t* __restrict__ perm_token,
                               float* __restrict__ perm_w) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -128,7 +131,7 @@ __device__ void scatter_chunk(const TokenPicks& pk, int T, int t0, int64_t offse
   if (threadIdx.x < kELocal) {
     int acc = sh.running[threadIdx.x];
 #pragma unroll
-    for (int w = 0; w < kRouteWaves; ++w) {
+    for (int w = 0; w < kPW; ++w) {
       sh.wave_base[w][threadIdx.x] = acc;
       acc += sh.wave_cnt[w][threadIdx.x];
     }
@@ -212,20 +215,24 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
   if (threadIdx.x < kELocal) block_hist[(size_t)blockIdx.x * kELocal + threadIdx.x] = hist[threadIdx.x];
 }
 
-// Permutation for T > 16: workgroup c handles tokens [1024c, 1024c + 1024).
-// Every workgroup reduces the route histograms to the per-expert totals and to
-// the counts of the tokens before its chunk; workgroup 0 writes expert_off.
-__global__ void __launch_bounds__(kRouteThreads)
+// Permutation for T > 16: workgroup c of kPW waves handles tokens
+// [64 kPW c, 64 kPW (c + 1)).  Every workgroup reduces the route histograms to
+// the per-expert totals and to the counts of the tokens before its chunk;
+// workgroup 0 writes expert_off.  T <= 64 takes one wave (kPW = 1): sixteen
+// waves spent ~4 us more on their per-expert ballot loops and barriers.
+template <int kPW>
+__global__ void __launch_bounds__(kPW * kWave)
 perm_kernel(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int T, int64_t offset,
             const int32_t* __restrict__ block_hist, int tokens_per_block, int32_t* __restrict__ pair_row,
             int32_t* __restrict__ expert_off, int32_t* __restrict__ perm_token, float* __restrict__ perm_w) {
-  constexpr int kGroups = kRouteThreads / kELocal;  // 32
-  __shared__ PermShared sh;
+  constexpr int kThreads = kPW * kWave;
+  constexpr int kGroups = kThreads / kELocal;
+  __shared__ PermShared<kPW> sh;
   __shared__ int part_tot[kGroups][kELocal];
   __shared__ int part_pre[kGroups][kELocal];
   const int nb = (T + tokens_per_block - 1) / tokens_per_block;
-  const int first = blockIdx.x * (kRouteThreads / tokens_per_block);  // route workgroups before this chunk
-  const TokenPicks pk0 = load_picks(ids, topk_w, T, blockIdx.x * kRouteThreads + threadIdx.x);
+  const int first = blockIdx.x * (kThreads / tokens_per_block);  // route workgroups before this chunk
+  const TokenPicks pk0 = load_picks(ids, topk_w, T, blockIdx.x * kThreads + threadIdx.x);
   const int e = threadIdx.x % kELocal;
   const int g = threadIdx.x / kELocal;
   int tot = 0, pre = 0;
@@ -268,7 +275,7 @@ perm_kernel(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, i
   __syncthreads();
   if (threadIdx.x < kWave) expert_offsets(sh, blockIdx.x == 0, expert_off);
   __syncthreads();
-  scatter_chunk(pk, T, blockIdx.x * kRouteThreads, offset, sh, pair_row, perm_token, perm_w);
+  scatter_chunk(pk, T, blockIdx.x * kThreads, offset, sh, pair_row, perm_token, perm_w);
 }
 
 }  // namespace
@@ -295,9 +302,14 @@ hipError_t launch_route(const float* logits, const uint16_t* bias, float rsf, in
   else
     hipLaunchKernelGGL((route_kernel<kRouteWaves, false>), dim3(blocks), dim3(kRouteThreads), 0, stream, logits,
                        bias, rsf, T, offset, ids, w, pair_row, off, perm_token, perm_w, hist);
-  const int chunks = (T + kRouteThreads - 1) / kRouteThreads;
-  hipLaunchKernelGGL(perm_kernel, dim3(chunks), dim3(kRouteThreads), 0, stream, (const int32_t*)ids,
-                     (const float*)w, T, offset, (const int32_t*)hist, tpb, pair_row, off, perm_token, perm_w);
+  if (T <= kWave) {
+    hipLaunchKernelGGL(perm_kernel<1>, dim3(1), dim3(kWave), 0, stream, (const int32_t*)ids, (const float*)w, T,
+                       offset, (const int32_t*)hist, tpb, pair_row, off, perm_token, perm_w);
+  } else {
+    const int chunks = (T + kRouteThreads - 1) / kRouteThreads;
+    hipLaunchKernelGGL(perm_kernel<kRouteWaves>, dim3(chunks), dim3(kRouteThreads), 0, stream, (const int32_t*)ids,
+                       (const float*)w, T, offset, (const int32_t*)hist, tpb, pair_row, off, perm_token, perm_w);
+  }
   return hipGetLastError();
 }
 
