@@ -613,7 +613,7 @@ hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, c
 //   * the workgroup's 128 gate columns (and its 128 up columns) are one
 //     128-column weight scale block, so one gate and one up scale per K block;
 //   * two LDS stages of 66 KB: the copy of K block kb + 1 runs while K block
-//     kb is multiplied;
+//     kb is multiplied, its DMAs issued between the first MFMAs;
 //   * the DMA sources are a wave-uniform base plus a 32-bit lane offset
 //     (saddr form), one VGPR per copied plane.
 // ---------------------------------------------------------------------------
@@ -698,17 +698,20 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
       (uint32_t)perm_token[row0 + min(wave * C::kScaleRowsPerWave + (lane < C::kScaleRowsPerWave ? lane : 0), rows - 1)];
   const int sdst = C::kSOff + wave * kWave * 4;
 
-  auto issue = [&](int kb) {
+  auto issue_plane = [&](int kb, int k) {
     char* base = lds + (kb & 1) * C::kStageBytes;
-    const uint8_t* hk = hs + kb * kBlk;
-    const uint8_t* wk = w13e + kb * kBlk;
+    const bool a_plane = k < C::kPlanesPerWave / 2;
+    const uint8_t* src = a_plane ? hs + kb * kBlk : w13e + kb * kBlk;
+    // A fragments wholly past the tile's rows are never read: no copy
+    if (!a_plane || ((wave + k * C::kWaves) >> 1) * 16 < rows) dma16(src + off[k], base + dst[k]);
+  };
+  auto issue_scale = [&](int kb) {
+    dma4(hs_scale + (size_t)kb * T + stok, lds + (kb & 1) * C::kStageBytes + sdst);
+  };
+  auto issue = [&](int kb) {
 #pragma unroll
-    for (int k = 0; k < C::kPlanesPerWave; ++k) {
-      const bool a_plane = k < C::kPlanesPerWave / 2;
-      // A fragments wholly past the tile's rows are never read: no copy
-      if (!a_plane || ((wave + k * C::kWaves) >> 1) * 16 < rows) dma16((a_plane ? hk : wk) + off[k], base + dst[k]);
-    }
-    dma4(hs_scale + (size_t)kb * T + stok, base + sdst);
+    for (int k = 0; k < C::kPlanesPerWave; ++k) issue_plane(kb, k);
+    issue_scale(kb);
   };
 
   // weight block scales of the tile's gate block and up block, per K block
@@ -724,7 +727,12 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
 #pragma unroll
     for (int nj = 0; nj < 2 * C::NJ; ++nj) acc[mi][nj] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int kb) {
+  // Multiply stage kb; with kc >= 0 also copy stage kc, its DMAs spread over
+  // the first column blocks (two planes behind each block's first MFMAs):
+  // issued as one burst after the barrier, they filled the memory pipeline
+  // and every wave stalled in the issue before its first MFMA (T = 8192:
+  // 1,198 -> 1,103 us; one plane per block needed more registers than fit).
+  auto compute = [&](int kb, int kc) {
     const char* sb = lds + (kb & 1) * C::kStageBytes;
     auto frag = [&](int off_) {
       const char* f = sb + off_;
@@ -744,6 +752,7 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
     v8i a[C::MI];
 #pragma unroll
     for (int mi = 0; mi < C::MI; ++mi) a[mi] = frag((C::MI * wm + mi) * C::kFrag);
+    if (kc >= 0) issue_scale(kc);
     float sgm[C::MI], sum[C::MI];  // row scale x gate / up weight scale
     auto read_scales = [&]() {
       const float sg = wsc[kb], su = wsc[kNHBlk + kb];
@@ -770,6 +779,11 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
         for (int mi = 2 * h; mi < 2 * h + 2; ++mi) pc[mi] = mfma_f8_16x16x128(bn, a[mi]);
+        if (h == 0 && kc >= 0) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            if (2 * nj + q < C::kPlanesPerWave) issue_plane(kc, 2 * nj + q);
+        }
         if (h == 1 && nj + 1 < 2 * C::NJ) bn = bfrag(nj + 1);
         if (h == 1 && nj == 0) read_scales();
         if (nj > 0) {
@@ -804,12 +818,14 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
   for (int kb = 0; kb < kNHBlk - 1; ++kb) {
     wait_vmcnt_lgkm0<0>();
     block_barrier();
-    issue(kb + 1);
-    if (wave_live) compute(kb);
+    if (wave_live)
+      compute(kb, kb + 1);
+    else
+      issue(kb + 1);
   }
   wait_vmcnt_lgkm0<0>();
   block_barrier();
-  if (wave_live) compute(kNHBlk - 1);
+  if (wave_live) compute(kNHBlk - 1, -1);
 
   // ---- SwiGLU epilogue (moe.py:190-193): act = silu(up) * gate ------------
 #pragma unroll
