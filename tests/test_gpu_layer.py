@@ -120,6 +120,10 @@ INTERMEDIATE_CASES = [
     ("skewed_t8192", 64, None),         # row-streaming kernels, experts of up to 64 rows
     ("prefill_t1024", None, 200),
     ("skewed_t8192", 2304, 160),        # LDS-tiled / wide kernels, ragged last tiles
+    # tiled GEMM2 with experts of a few to ~40 rows, every row: 16-row blocks
+    # past a tile's rows are skipped per wave (0, 1 or 2 live blocks)
+    ("prefill_t1024", 320, None),
+    ("small_t64", 256, None),
 ]
 
 
