@@ -15,11 +15,12 @@
 //     groups are ranked one per lane, and the top-8 is a rank of the few
 //     candidates at or above the kept groups' least second-largest key (DPP
 //     row rotations), in expert order (route_token_lanes);
-//   * T <= 16 (decode): the single workgroup also builds the permutation from
-//     LDS (per-expert token bitmasks), with no global atomics, fences or
-//     re-reads of the ids (route_small, route_token.hpp).  The layer itself
-//     runs that routing inside GEMM1 for T <= 16; this kernel serves the
-//     routing-only entry point there;
+//   * T <= 24: one workgroup routes every token (a wave per token, up to two
+//     tokens per wave) and builds the permutation from LDS (per-expert token
+//     bitmasks), with no global atomics, fences or re-reads of the ids
+//     (route_small, route_token.hpp), in one launch instead of two.  The
+//     layer itself runs that routing inside GEMM1 for T <= 16; this kernel
+//     serves the routing-only entry point there;
 //   * larger T: each workgroup stores its local-expert histogram (plain
 //     stores, no atomics); a second kernel (one workgroup per 1024 tokens)
 //     reduces the histograms to the expert row offsets and the per-chunk bases
@@ -32,8 +33,13 @@
 namespace moe {
 namespace {
 
-constexpr int kRouteWaves = 16;      // tokens per route workgroup, T <= 16 (single workgroup)
-constexpr int kRouteWavesMulti = 4;  // tokens per route workgroup, 16 < T <= kRouteMultiSmallMaxTokens
+constexpr int kRouteWaves = 16;      // waves per route workgroup (T > 1024: a token each)
+// T <= 24: one workgroup routes and permutes every token, a wave per token
+// (a second token for some waves), in one launch instead of two: T = 17
+// 11.7 -> 9.4 us, T = 24 12.2 -> 10.6 us.  Beyond, a wave's routing chains
+// in sequence cost more than the second launch (T = 32 +1.4 us, T = 64 +7).
+constexpr int kRouteSingleMaxTokens = 24;
+constexpr int kRouteWavesMulti = 4;  // tokens per route workgroup, 24 < T <= kRouteMultiSmallMaxTokens
 constexpr int kRouteMultiSmallMaxTokens = 1024;
 constexpr int kRouteThreads = kRouteWaves * kWave;
 
@@ -185,8 +191,8 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
              int32_t* __restrict__ perm_token, float* __restrict__ perm_w, int32_t* __restrict__ block_hist) {
   static_assert(kW == kRouteWaves || (kW == kRouteWavesMulti && !kSingle), "route workgroup shapes");
   if constexpr (kSingle) {
-    static_assert(kW == kSmallRouteMaxTokens, "one wave per token");
-    __shared__ SmallRoute sr;
+    static_assert(kW == kSmallRouteMaxWaves, "the workgroup shape route_small is sized for");
+    __shared__ SmallRouteT<kRouteSingleMaxTokens> sr;
     const RouteOut out{ids, w, pair_row, expert_off, perm_token, perm_w};
     route_small(logits, bias, rsf, T, offset, sr, out, true);
     return;
@@ -289,7 +295,7 @@ hipError_t launch_route(const float* logits, const uint16_t* bias, float rsf, in
   int32_t* perm_token = (int32_t*)(ws + L.perm_token);
   float* perm_w = (float*)(ws + L.perm_w);
   int32_t* hist = (int32_t*)(ws + L.block_hist);
-  if (T <= kRouteWaves) {
+  if (T <= kRouteSingleMaxTokens) {
     hipLaunchKernelGGL((route_kernel<kRouteWaves, true>), dim3(1), dim3(kRouteThreads), 0, stream, logits, bias,
                        rsf, T, offset, ids, w, pair_row, off, perm_token, perm_w, hist);
     return hipGetLastError();

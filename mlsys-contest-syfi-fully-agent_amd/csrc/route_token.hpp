@@ -1,6 +1,6 @@
 // route_token.hpp -- DeepSeek-V3 grouped routing of one token by one
 // wavefront (moe.py:123-158), and the whole routing with the permutation for
-// up to 16 tokens in one workgroup (moe.py:168-179).  Used by the routing
+// up to 24 tokens in one workgroup (moe.py:168-179).  Used by the routing
 // kernels and by GEMM1's decode path, which routes its few tokens itself
 // instead of waiting for a routing launch.
 #pragma once
@@ -173,22 +173,26 @@ __device__ inline void route_token(const float* __restrict__ logits, const uint1
 }
 
 // ---------------------------------------------------------------------------
-// Routing and permutation of T <= 16 tokens in one workgroup, from LDS only
-// (no global round trip of the ids).  Token t is routed by wave t % waves.
-// Rows of local expert le are its tokens in ascending order (moe.py:168-179),
-// starting at the exclusive scan of the per-expert counts.  `sr` is LDS of
-// the caller (inside its single LDS object); the workspace outputs `out`
-// are written only when `write_out` is set.
+// Routing and permutation of T <= kMaxT tokens in one workgroup, from LDS
+// only (no global round trip of the ids).  Token t is routed by wave
+// t % waves.  Rows of local expert le are its tokens in ascending order
+// (moe.py:168-179), starting at the exclusive scan of the per-expert counts.
+// `sr` is LDS of the caller (inside its single LDS object); the workspace
+// outputs `out` are written only when `write_out` is set.  GEMM1's decode
+// path routes up to 16 tokens this way, the routing launch up to 24.
 // ---------------------------------------------------------------------------
 constexpr int kSmallRouteMaxTokens = 16;
+constexpr int kSmallRouteMaxWaves = 16;
 
-struct SmallRoute {
+template <int kMaxT>
+struct SmallRouteT {
+  static_assert(kMaxT <= 32, "token masks are 32 bits");
   uint32_t tokmask[kELocal];                       // bit t: token t chose local expert le
   int expert_off[kELocal + 1];                     // first row per local expert; [32] = rows
-  int pair_id[kSmallRouteMaxTokens][kTopK];        // selected global ids, ascending
-  float pair_w[kSmallRouteMaxTokens][kTopK];       // their weights
-  int perm_token[kSmallRouteMaxTokens * kTopK];    // token of each permuted row
-  float perm_w[kSmallRouteMaxTokens * kTopK];      // weight of each permuted row
+  int pair_id[kMaxT][kTopK];                       // selected global ids, ascending
+  float pair_w[kMaxT][kTopK];                      // their weights
+  int perm_token[kMaxT * kTopK];                   // token of each permuted row
+  float perm_w[kMaxT * kTopK];                     // weight of each permuted row
   // T == 1 (route_one): the token's 32-bit keys, sigmoid scores, group scores,
   // each group's second largest key, and the compacted top-8 candidates
   uint32_t key1[kEGlobal];
@@ -197,9 +201,10 @@ struct SmallRoute {
   uint32_t gb1[kNGroup];
   uint64_t cand[16];
   // T >= 2 (route_token_lanes, a wave per token): each wave's top-8 candidates
-  uint64_t cand_w[kSmallRouteMaxTokens][16];
-  float cand_sw[kSmallRouteMaxTokens][16];
+  uint64_t cand_w[kSmallRouteMaxWaves][16];
+  float cand_sw[kSmallRouteMaxWaves][16];
 };
+using SmallRoute = SmallRouteT<kSmallRouteMaxTokens>;
 
 struct RouteOut {
   int32_t* ids;
@@ -347,8 +352,9 @@ __device__ inline void route_token_lanes(const float* __restrict__ logits, const
 // the kept groups only (two keys per lane in wave 0), then the permutation
 // of the single token written directly.  Needs at least 4 waves; ends with
 // a workgroup barrier.
+template <int kMaxT>
 __device__ inline void route_one(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf,
-                                 int64_t offset, SmallRoute& sr, RouteOut out, bool write_out) {
+                                 int64_t offset, SmallRouteT<kMaxT>& sr, RouteOut out, bool write_out) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   if (wave < 4) {
@@ -505,8 +511,9 @@ __device__ inline void route_one(const float* __restrict__ logits, const uint16_
   __syncthreads();
 }
 
+template <int kMaxT>
 __device__ inline void route_small(const float* __restrict__ logits, const uint16_t* __restrict__ bias, float rsf,
-                                   int T, int64_t offset, SmallRoute& sr, RouteOut out, bool write_out) {
+                                   int T, int64_t offset, SmallRouteT<kMaxT>& sr, RouteOut out, bool write_out) {
   if (T == 1) {
     route_one(logits, bias, rsf, offset, sr, out, write_out);
     return;

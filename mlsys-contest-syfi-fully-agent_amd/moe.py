@@ -29,6 +29,11 @@ H, I, E_LOCAL, E_GLOBAL, TOP_K, BLOCK = 7168, 2048, 32, 256, 8, 128
 # workspace holds no GEMM2 rows (`down`; kGemm2StreamMaxTokens in
 # csrc/moe_common.hpp).
 FUSED_COMBINE_MAX_TOKENS = 64
+# Up to this T one workgroup routes the tokens and builds the permutation
+# (inside GEMM1 for T <= 16 in the layer), so the workspace holds no
+# per-workgroup routing histograms (`block_hist`; kRouteSingleMaxTokens in
+# csrc/route.hip).
+ROUTE_ONE_WORKGROUP_MAX_TOKENS = 24
 
 _ws_lock = threading.Lock()
 _ws: dict = {}
@@ -192,8 +197,10 @@ class RouteResult:
         self.down = (view(lay.down, T * TOP_K * H, torch.float32).view(T * TOP_K, H)
                      if T > FUSED_COMBINE_MAX_TOKENS else None)
         # one row per routing workgroup: 4 tokens each up to T = 1024, 16 beyond
+        # (written only where a permutation launch reads them)
         blocks = (T + 3) // 4 if T <= 1024 else (T + 15) // 16
-        self.block_hist = view(lay.block_hist, blocks * E_LOCAL, torch.int32).view(-1, E_LOCAL)
+        self.block_hist = (view(lay.block_hist, blocks * E_LOCAL, torch.int32).view(-1, E_LOCAL)
+                           if T > ROUTE_ONE_WORKGROUP_MAX_TOKENS else None)
 
 
 def route(routing_logits, routing_bias, local_expert_offset, routed_scaling_factor, ws=None):

@@ -63,6 +63,17 @@ def test_max_tokens_keeps_row_offsets_in_32_bits(pkg):
     assert L.moe_fp8_ds_workspace_size(tmax) > 0
 
 
+def test_python_thresholds_match_the_kernels(pkg):
+    """The Python views' kernel thresholds are the ones the sources use."""
+    csrc = os.path.join(ROOT, "mlsys-contest-syfi-fully-agent_amd", "csrc")
+    common = open(os.path.join(csrc, "moe_common.hpp")).read()
+    route = open(os.path.join(csrc, "route.hip")).read()
+    assert re.search(r"constexpr int kGemm2StreamMaxTokens = (\d+);", common).group(1) == \
+        str(pkg.moe.FUSED_COMBINE_MAX_TOKENS)
+    assert re.search(r"constexpr int kRouteSingleMaxTokens = (\d+);", route).group(1) == \
+        str(pkg.moe.ROUTE_ONE_WORKGROUP_MAX_TOKENS)
+
+
 def test_noalloc_validation_without_gpu(pkg):
     """moe_fp8_ds_run_noalloc refuses T beyond its scratch before any HIP call."""
     L = pkg._lib.moe_lib()

@@ -46,6 +46,8 @@ LAYER_CASES = [
     ("prefill_t1024", 256, 128, None),
     # token counts on either side of each kernel-choice boundary
     ("small_t64", None, 17, None),        # first T past the in-GEMM1 routing
+    ("small_t64", None, 24, None),        # largest T of the one-workgroup routing launch
+    ("small_t64", None, 25, None),        # routing plus a permutation launch
     # streaming kernels with experts of more than 16 rows (four hot experts of
     # up to 64 and 40 rows: the row-tile loops)
     ("skewed_t8192", None, 64, None),

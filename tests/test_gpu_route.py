@@ -20,6 +20,9 @@ CASES = [
     ("prefill_t1024", -16, None),   # window partly below expert 0
     ("prefill_t1024", 256, None),   # no local expert at all
     ("small_t64", 96, 3),           # T not a multiple of the 4-token block
+    ("small_t64", None, 17),        # one workgroup routes and permutes (T <= 24)
+    ("prefill_t1024", None, 24),    # largest T of the one-workgroup routing
+    ("prefill_t1024", None, 25),    # smallest T of routing plus a permutation launch
     ("skewed_t8192", 64, 777),      # ragged, large
 ]
 
@@ -78,10 +81,12 @@ def test_route_matches_oracle(pkg, orc, cuda_device, name, offset, T):
                 assert pw[row] == w[t, k]
             else:
                 assert pair[t, k] == -1
-    # per-workgroup histograms (T > 16 uses the two-kernel path) add up to the
+    # per-workgroup histograms (the two-launch path, T > 24) add up to the
     # expert counts
-    if T > 16:
+    if T > pkg.moe.ROUTE_ONE_WORKGROUP_MAX_TOKENS:
         np.testing.assert_array_equal(r.block_hist.cpu().numpy().sum(axis=0), counts)
+    else:
+        assert r.block_hist is None
 
 
 def test_route_repeatable(pkg, cuda_device):
