@@ -16,6 +16,8 @@
 //   * streaming (small T): one workgroup per (expert, 8-column group), weights
 //     read once straight into registers -- HBM-bound;
 //   * tiled (large T): LDS-staged operand tiles, DMA pipeline -- MFMA-bound.
+#include <type_traits>
+
 #include "route_token.hpp"
 
 namespace moe {
@@ -709,19 +711,24 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
       (uint32_t)perm_token[row0 + min(wave * C::kScaleRowsPerWave + (lane < C::kScaleRowsPerWave ? lane : 0), rows - 1)];
   const int sdst = C::kSOff + wave * kWave * 4;
 
-  auto issue_plane = [&](int kb, int k) {
+  auto issue_plane = [&](int kb, int k, auto nt_c) {
     char* base = lds + (kb & 1) * C::kStageBytes;
     const bool a_plane = k < C::kPlanesPerWave / 2;
-    const uint8_t* src = a_plane ? hs + kb * kBlk : w13e + kb * kBlk;
-    // A fragments wholly past the tile's rows are never read: no copy
-    if (!a_plane || ((wave + k * C::kWaves) >> 1) * 16 < rows) dma16(src + off[k], base + dst[k]);
+    if (a_plane) {
+      // A fragments wholly past the tile's rows are never read: no copy
+      if (((wave + k * C::kWaves) >> 1) * 16 < rows) dma16(hs + kb * kBlk + off[k], base + dst[k]);
+    } else if constexpr (decltype(nt_c)::value) {
+      dma16_nt(w13e + kb * kBlk + off[k], base + dst[k]);
+    } else {
+      dma16(w13e + kb * kBlk + off[k], base + dst[k]);
+    }
   };
   auto issue_scale = [&](int kb) {
     dma4(hs_scale + (size_t)kb * T + stok, lds + (kb & 1) * C::kStageBytes + sdst);
   };
-  auto issue = [&](int kb) {
+  auto issue = [&](int kb, auto nt_c) {
 #pragma unroll
-    for (int k = 0; k < C::kPlanesPerWave; ++k) issue_plane(kb, k);
+    for (int k = 0; k < C::kPlanesPerWave; ++k) issue_plane(kb, k, nt_c);
     issue_scale(kb);
   };
 
@@ -743,7 +750,7 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
   // issued as one burst after the barrier, they filled the memory pipeline
   // and every wave stalled in the issue before its first MFMA (T = 8192:
   // 1,198 -> 1,103 us; one plane per block needed more registers than fit).
-  auto compute = [&](int kb, int kc) {
+  auto compute = [&](int kb, int kc, auto nt_c) {
     const char* sb = lds + (kb & 1) * C::kStageBytes;
     auto frag = [&](int off_) {
       const char* f = sb + off_;
@@ -793,7 +800,7 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
         if (h == 0 && kc >= 0) {
 #pragma unroll
           for (int q = 0; q < 2; ++q)
-            if (2 * nj + q < C::kPlanesPerWave) issue_plane(kc, 2 * nj + q);
+            if (2 * nj + q < C::kPlanesPerWave) issue_plane(kc, 2 * nj + q, nt_c);
         }
         if (h == 1 && nj + 1 < 2 * C::NJ) bn = bfrag(nj + 1);
         if (h == 1 && nj == 0) read_scales();
@@ -824,19 +831,29 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
   // Step kb: stage kb has landed (the only copy in flight) and every wave has
   // finished reading stage kb - 1, so after the barrier that buffer takes the
   // copy of stage kb + 1 while stage kb is multiplied.
-  issue(0);
+  auto run = [&](auto nt_c) {
+    issue(0, nt_c);
 #pragma unroll 1
-  for (int kb = 0; kb < kNHBlk - 1; ++kb) {
+    for (int kb = 0; kb < kNHBlk - 1; ++kb) {
+      wait_vmcnt_lgkm0<0>();
+      block_barrier();
+      if (wave_live)
+        compute(kb, kb + 1, nt_c);
+      else
+        issue(kb + 1, nt_c);
+    }
     wait_vmcnt_lgkm0<0>();
     block_barrier();
-    if (wave_live)
-      compute(kb, kb + 1);
-    else
-      issue(kb + 1);
-  }
-  wait_vmcnt_lgkm0<0>();
-  block_barrier();
-  if (wave_live) compute(kNHBlk - 1, -1);
+    if (wave_live) compute(kNHBlk - 1, -1, nt_c);
+  };
+  // The W13 tile of an expert that fits one row tile is read exactly once:
+  // nontemporal copies, a loop of their own (a branch per copy made the
+  // kernel spill).  T = 1025: GEMM1 206.6 -> 191.8 us, T = 4096 302.8 ->
+  // 291.6 us; T = 8192 unchanged (its hot experts span many row tiles).
+  if (X.end(e) - X.begin(e) <= C::BM)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
 
   // ---- SwiGLU epilogue (moe.py:190-193): act = silu(up) * gate ------------
 #pragma unroll
