@@ -61,14 +61,34 @@ __device__ __forceinline__ S2Job s2_next(const ExpertRows& X, uint32_t active, S
   return later ? S2Job{__builtin_ctz(later), 0} : S2Job{-1, 0};
 }
 
+// A job's act operands, 16 slots: slot c = ((k * 2 + g) * 2 + h) * 2 + part
+// holds, in lane (q, r), row r's columns (kb0 + k) * 128 + 64 g + 16 q + 8 h
+// .. +7 (64-column chunk 2 (kb0 + k) + g), the bf16 hi half (part 0) or the
+// lo half (part 1, 64 elements further in the act row).
+static_assert(kS2KB == 2, "16 act operand slots per job");
+constexpr int kS2Slots = 8 * kS2KB;
+constexpr int s2_slot(int k, int g, int h, int part) { return ((k * 2 + g) * 2 + h) * 2 + part; }
+__device__ __forceinline__ int s2_slot_off(int c) {
+  return (2 * (c >> 3) + ((c >> 2) & 1)) * 128 + 8 * ((c >> 1) & 1) + 64 * (c & 1);
+}
+
 struct S2Regs {
-  v4i a[kS2KB][2][2];  // act hi: columns 64g + 16q + 8h .. +7 of each of this wave's scale blocks
-  v4i al[kS2KB][2][2]; // act lo, same columns
+  v4i op[kS2Slots];  // act operands (kFew: spread over op[0..3], see s2_load)
   float sw[kS2KB];
   int tok;           // token and weight of the row this thread combines
   float pw;          //   (row = (tid / 16) % 16 of the tile)
 };
 
+// Loads a job's act rows.  The loads cost per instruction, not per lane: a
+// job of one to four rows took 16 of them for 16 rows, on the path its W2
+// copies share (small_t64: 18 of GEMM2's 63 us).  kFew (every expert of the
+// launch has at most four rows, so every job): all 16 slots in 4
+// instructions, lane (q, r) taking row r % 4 of slot 4i + r / 4;
+// s2_operand moves them into the MFMA lanes once they have landed.  Chosen
+// per launch, not per job: a branch per job made the compiler merge the two
+// layouts of the persistent operand registers and wait for every load in
+// flight before the next job's loads.
+template <bool kFew>
 __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
                                         const int32_t* __restrict__ perm_token, const float* __restrict__ perm_w,
                                         const uint16_t* __restrict__ act, const float* __restrict__ w2_scale, int n0,
@@ -79,21 +99,70 @@ __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
   const int crow = row0 + min((int)(threadIdx.x >> 4) & 15, rows - 1);
   R.tok = perm_token[crow];
   R.pw = perm_w[crow];
-  const uint16_t* ap = act + (size_t)(row0 + min(lr, rows - 1)) * kActRowElems + 16 * lq;
+  const uint16_t* ab = act + (size_t)kb0 * 256 + 16 * lq;  // + row * kActRowElems + s2_slot_off(slot)
+  if constexpr (kFew) {
+    const uint16_t* ap = ab + (size_t)(row0 + min(lr & 3, rows - 1)) * kActRowElems;
 #pragma unroll
-  for (int k = 0; k < kS2KB; ++k) {
+    for (int i = 0; i < kS2Slots / 4; ++i) R.op[i] = *(const v4i*)(ap + s2_slot_off(4 * i + (lr >> 2)));
+  } else {
+    const uint16_t* ap = ab + (size_t)(row0 + min(lr, rows - 1)) * kActRowElems;
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+    for (int c = 0; c < kS2Slots; ++c) R.op[c] = *(const v4i*)(ap + s2_slot_off(c));
+  }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        // column (kb0 + k) * 128 + 64 g + 16 q + 8 h: 64-column chunk 2 (kb0 + k) + g
-        const uint16_t* c = ap + (2 * (kb0 + k) + g) * 128 + 8 * h;
-        R.a[k][g][h] = *(const v4i*)c;
-        R.al[k][g][h] = *(const v4i*)(c + 64);
-      }
-    R.sw[k] = w2_scale[((size_t)j.e * kNHBlk + n0 / kBlk) * kNIBlk + kb0 + k];
+  for (int k = 0; k < kS2KB; ++k) R.sw[k] = w2_scale[((size_t)j.e * kNHBlk + n0 / kBlk) * kNIBlk + kb0 + k];
+}
+
+// v4i of lane r + N of the lane's 16-lane row (DPP row_shl:N; lanes past the
+// row's end read 0 and feed only discarded rows).
+template <int N>
+__device__ __forceinline__ v4i row_shl(const v4i& x) {
+  if constexpr (N == 0) {
+    return x;
+  } else {
+    return v4i{__builtin_amdgcn_mov_dpp(x[0], 0x100 + N, 0xF, 0xF, true),
+               __builtin_amdgcn_mov_dpp(x[1], 0x100 + N, 0xF, 0xF, true),
+               __builtin_amdgcn_mov_dpp(x[2], 0x100 + N, 0xF, 0xF, true),
+               __builtin_amdgcn_mov_dpp(x[3], 0x100 + N, 0xF, 0xF, true)};
   }
 }
+
+// Operand slot C of a landed job in the MFMA layout (lane (q, r): row r); kFew:
+// slot C sits in op[C / 4], lanes shifted by 4 (C % 4).  Template constants:
+// a shift chosen at run time (folded only after unrolling) left the operands
+// in scratch memory.
+template <bool kFew, int C>
+__device__ __forceinline__ v4i s2_operand(const S2Regs& R) {
+  if constexpr (kFew)
+    return row_shl<4 * (C % 4)>(R.op[C / 4]);
+  else
+    return R.op[C];
+}
+
+// s2_operand for the unrolled (k, g, h, part) of the MFMA loop: the 16 slot
+// constants spelled out, so that every shift is a template constant.
+template <bool kFew>
+__device__ __forceinline__ v4i s2_op(const S2Regs& R, int k, int g, int h, int part) {
+  switch (s2_slot(k, g, h, part)) {
+    case 0: return s2_operand<kFew, 0>(R);
+    case 1: return s2_operand<kFew, 1>(R);
+    case 2: return s2_operand<kFew, 2>(R);
+    case 3: return s2_operand<kFew, 3>(R);
+    case 4: return s2_operand<kFew, 4>(R);
+    case 5: return s2_operand<kFew, 5>(R);
+    case 6: return s2_operand<kFew, 6>(R);
+    case 7: return s2_operand<kFew, 7>(R);
+    case 8: return s2_operand<kFew, 8>(R);
+    case 9: return s2_operand<kFew, 9>(R);
+    case 10: return s2_operand<kFew, 10>(R);
+    case 11: return s2_operand<kFew, 11>(R);
+    case 12: return s2_operand<kFew, 12>(R);
+    case 13: return s2_operand<kFew, 13>(R);
+    case 14: return s2_operand<kFew, 14>(R);
+    default: return s2_operand<kFew, 15>(R);
+  }
+}
+
 
 // A job's W2 bytes of this wave (rows n0 .. n0 + 31, K blocks kb0, kb0 + 1)
 // -> the wave's LDS stage: per 16-row block and K block two wide planes (rows
@@ -153,86 +222,98 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
   // with a copy that could be skipped alone it merged the paths to vmcnt(0)
   // and so waited for the prefetch it had just issued, one full memory
   // latency per job (small_t64: 3.6 us per job, 2.1 of it that wait).
-  S2Job job = s2_next(X, active, {-1, 0});
-  S2Job j1 = job.e >= 0 ? s2_next(X, active, job) : job;
-  S2Regs r0, r1;
-  if (job.e >= 0) {
-    s2_load(r0, job, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
-    s2_copy_w(stage(0), job, w2, n0, kb0, lane);
-    s2_copy_w(stage(1), j1.e >= 0 ? j1 : job, w2, n0, kb0, lane);
-  }
-  // One job from stage `s` with act rows `cur`; after its MFMAs, loads the
-  // next job's act rows into `nxt` and starts the copy of the job after next
-  // into stage `s`.  Issue order is always: act rows of job j, copy of job
-  // j + 1.
-  auto step = [&](int s, const S2Regs& cur, S2Regs& nxt) {
-    // This job's W2 stage and act rows have landed; the next job's W2 copy
-    // (8 per lane, issued last) may stay in flight.
-    wait_vmcnt_lgkm0<2 * kS2KB * kS2NB>();
-    asm volatile("" ::: "memory");
-    v4i b[kS2NB][kS2KB][2];
-#pragma unroll
-    for (int nb = 0; nb < kS2NB; ++nb)
-#pragma unroll
-      for (int k = 0; k < kS2KB; ++k)
-#pragma unroll
-        for (int g = 0; g < 2; ++g)
-          b[nb][k][g] = *(const v4i*)(stage(s) + 2 * (nb * kS2KB + k) * 1024 + wide_slot(lr, 4 * g + lq));
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the stage is read: free for the job after next
-    const S2Job j2 = j1.e >= 0 ? s2_next(X, active, j1) : j1;
-#pragma unroll
-    for (int nb = 0; nb < kS2NB; ++nb) {
-      v4f acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k = 0; k < kS2KB; ++k) {
-        v4f p = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          const v8bf b0 = e4m3x8_to_bf16((uint32_t)b[nb][k][g][0], (uint32_t)b[nb][k][g][1]);
-          const v8bf b1 = e4m3x8_to_bf16((uint32_t)b[nb][k][g][2], (uint32_t)b[nb][k][g][3]);
-          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][0]), b0, p);
-          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.a[k][g][1]), b1, p);
-          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.al[k][g][0]), b0, p);
-          p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, cur.al[k][g][1]), b1, p);
+  // Every expert of the launch has at most four rows (every launch at T <= 4,
+  // decode among them): act rows spread over 4 loads per job (s2_load),
+  // one loop for the whole launch (decode_t1_s3 23.7 -> 22.6 us, T = 17
+  // 84.8 -> 79.0 us, same bits).
+  const bool few = __ballot(X.cnt > 4) == 0;
+  auto run = [&](auto few_c) {
+    constexpr bool kFew = decltype(few_c)::value;
+    S2Job job = s2_next(X, active, {-1, 0});
+    S2Job j1 = job.e >= 0 ? s2_next(X, active, job) : job;
+    S2Regs r0, r1;
+    if (job.e >= 0) {
+      s2_load<kFew>(r0, job, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
+      s2_copy_w(stage(0), job, w2, n0, kb0, lane);
+      s2_copy_w(stage(1), j1.e >= 0 ? j1 : job, w2, n0, kb0, lane);
+    }
+    // One job from stage `s` with act rows `cur`; after its MFMAs, loads the
+    // next job's act rows into `nxt` and starts the copy of the job after next
+    // into stage `s`.  Issue order is always: act rows of job j, copy of job
+    // j + 1.
+    auto step = [&](int s, const S2Regs& cur, S2Regs& nxt) {
+      // This job's W2 stage and act rows have landed; the next job's W2 copy
+      // (8 per lane, issued last) may stay in flight.
+      wait_vmcnt_lgkm0<2 * kS2KB * kS2NB>();
+      asm volatile("" ::: "memory");
+      v4i b[kS2NB][kS2KB][2];
+  #pragma unroll
+      for (int nb = 0; nb < kS2NB; ++nb)
+  #pragma unroll
+        for (int k = 0; k < kS2KB; ++k)
+  #pragma unroll
+          for (int g = 0; g < 2; ++g)
+            b[nb][k][g] = *(const v4i*)(stage(s) + 2 * (nb * kS2KB + k) * 1024 + wide_slot(lr, 4 * g + lq));
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the stage is read: free for the job after next
+      const S2Job j2 = j1.e >= 0 ? s2_next(X, active, j1) : j1;
+  #pragma unroll
+      for (int nb = 0; nb < kS2NB; ++nb) {
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+        for (int k = 0; k < kS2KB; ++k) {
+          v4f p = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+          for (int g = 0; g < 2; ++g) {
+            const v8bf b0 = e4m3x8_to_bf16((uint32_t)b[nb][k][g][0], (uint32_t)b[nb][k][g][1]);
+            const v8bf b1 = e4m3x8_to_bf16((uint32_t)b[nb][k][g][2], (uint32_t)b[nb][k][g][3]);
+            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<kFew>(cur, k, g, 0, 0)), b0, p);
+            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<kFew>(cur, k, g, 1, 0)), b1, p);
+            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<kFew>(cur, k, g, 0, 1)), b0, p);
+            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<kFew>(cur, k, g, 1, 1)), b1, p);
+          }
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], cur.sw[k], acc[i]);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], cur.sw[k], acc[i]);
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) red[(wave * kS2NB + nb) * 256 + (4 * lq + i) * 16 + lr] = acc[i];
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) red[(wave * kS2NB + nb) * 256 + (4 * lq + i) * 16 + lr] = acc[i];
-    }
-    // The next job's loads go out after this job's MFMAs: with the memory
-    // queue full their issue stalls, and the MFMAs no longer wait behind it
-    // (small_t64 GEMM2 62.5 -> 61.5 us).
-    if (j1.e >= 0) {
-      s2_load(nxt, j1, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
-      s2_copy_w(stage(s), j2.e >= 0 ? j2 : j1, w2, n0, kb0, lane);
-    }
-    lds_barrier();
-    {
-      // thread = (column block nb, row r, column c): every thread of the workgroup
-      static_assert(kS2Threads == kS2NB * 256, "one thread per output of a job");
-      const int nb = threadIdx.x >> 8, r = (threadIdx.x >> 4) & 15, c = threadIdx.x & 15;
-      const int row = X.begin(job.e) + job.rt * 16 + r;
-      if (row < X.end(job.e)) {
-        float o = red[nb * 256 + (threadIdx.x & 255)];
-#pragma unroll
-        for (int w = 1; w < kS2Waves; ++w) o += red[(w * kS2NB + nb) * 256 + (threadIdx.x & 255)];
-        const float p = o * cur.pw;
-        float& a = outacc[cur.tok * kS2Cols + 16 * nb + c];
-        a = a + p;
+      // The next job's loads go out after this job's MFMAs: with the memory
+      // queue full their issue stalls, and the MFMAs no longer wait behind it
+      // (small_t64 GEMM2 62.5 -> 61.5 us).
+      if (j1.e >= 0) {
+        s2_load<kFew>(nxt, j1, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
+        s2_copy_w(stage(s), j2.e >= 0 ? j2 : j1, w2, n0, kb0, lane);
       }
+      lds_barrier();
+      {
+        // thread = (column block nb, row r, column c): every thread of the workgroup
+        static_assert(kS2Threads == kS2NB * 256, "one thread per output of a job");
+        const int nb = threadIdx.x >> 8, r = (threadIdx.x >> 4) & 15, c = threadIdx.x & 15;
+        const int row = X.begin(job.e) + job.rt * 16 + r;
+        if (row < X.end(job.e)) {
+          float o = red[nb * 256 + (threadIdx.x & 255)];
+  #pragma unroll
+          for (int w = 1; w < kS2Waves; ++w) o += red[(w * kS2NB + nb) * 256 + (threadIdx.x & 255)];
+          const float p = o * cur.pw;
+          float& a = outacc[cur.tok * kS2Cols + 16 * nb + c];
+          a = a + p;
+        }
+      }
+      lds_barrier();
+      job = j1;
+      j1 = j2;
+    };
+  #pragma unroll 1
+    while (job.e >= 0) {
+      step(0, r0, r1);
+      if (job.e < 0) break;
+      step(1, r1, r0);
     }
-    lds_barrier();
-    job = j1;
-    j1 = j2;
   };
-#pragma unroll 1
-  while (job.e >= 0) {
-    step(0, r0, r1);
-    if (job.e < 0) break;
-    step(1, r1, r0);
-  }
+  if (few)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated copy lands before the LDS is released
   for (int i = threadIdx.x; i < T * kS2Cols; i += kS2Threads)
     out[(size_t)(i / kS2Cols) * kH + n0 + (i % kS2Cols)] = f32_to_bf16_rne(outacc[i]);
