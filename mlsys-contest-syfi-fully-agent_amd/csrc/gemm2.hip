@@ -73,7 +73,7 @@ __device__ __forceinline__ int s2_slot_off(int c) {
 }
 
 struct S2Regs {
-  v4i op[kS2Slots];  // act operands (kFew: spread over op[0..3], see s2_load)
+  v4i op[kS2Slots];  // act operands (spread S > 0: over op[0 .. 16 / 2^S), see s2_load)
   float sw[kS2KB];
   int tok;           // token and weight of the row this thread combines
   float pw;          //   (row = (tid / 16) % 16 of the tile)
@@ -81,14 +81,15 @@ struct S2Regs {
 
 // Loads a job's act rows.  The loads cost per instruction, not per lane: a
 // job of one to four rows took 16 of them for 16 rows, on the path its W2
-// copies share (small_t64: 18 of GEMM2's 63 us).  kFew (every expert of the
-// launch has at most four rows, so every job): all 16 slots in 4
-// instructions, lane (q, r) taking row r % 4 of slot 4i + r / 4;
-// s2_operand moves them into the MFMA lanes once they have landed.  Chosen
-// per launch, not per job: a branch per job made the compiler merge the two
-// layouts of the persistent operand registers and wait for every load in
-// flight before the next job's loads.
-template <bool kFew>
+// copies share (small_t64: 18 of GEMM2's 63 us).  Spread S: every expert of
+// the launch has at most 16 / 2^S rows (so every job), and the 16 slots take
+// 16 / 2^S instructions, lane (q, r) taking row r mod 16 / 2^S of slot
+// 2^S i + r / (16 / 2^S) (S = 2: row r % 4 of slot 4i + r / 4); s2_operand
+// moves them into the MFMA lanes once they have landed.  Chosen per launch,
+// not per job: a branch per job made the compiler merge two layouts of the
+// persistent operand registers and wait for every load in flight before the
+// next job's loads.
+template <int S>
 __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
                                         const int32_t* __restrict__ perm_token, const float* __restrict__ perm_w,
                                         const uint16_t* __restrict__ act, const float* __restrict__ w2_scale, int n0,
@@ -100,15 +101,10 @@ __device__ __forceinline__ void s2_load(S2Regs& R, S2Job j, const ExpertRows& X,
   R.tok = perm_token[crow];
   R.pw = perm_w[crow];
   const uint16_t* ab = act + (size_t)kb0 * 256 + 16 * lq;  // + row * kActRowElems + s2_slot_off(slot)
-  if constexpr (kFew) {
-    const uint16_t* ap = ab + (size_t)(row0 + min(lr & 3, rows - 1)) * kActRowElems;
+  constexpr int kRows = 16 >> S;  // rows one load instruction covers
+  const uint16_t* ap = ab + (size_t)(row0 + min(lr & (kRows - 1), rows - 1)) * kActRowElems;
 #pragma unroll
-    for (int i = 0; i < kS2Slots / 4; ++i) R.op[i] = *(const v4i*)(ap + s2_slot_off(4 * i + (lr >> 2)));
-  } else {
-    const uint16_t* ap = ab + (size_t)(row0 + min(lr, rows - 1)) * kActRowElems;
-#pragma unroll
-    for (int c = 0; c < kS2Slots; ++c) R.op[c] = *(const v4i*)(ap + s2_slot_off(c));
-  }
+  for (int i = 0; i < kS2Slots >> S; ++i) R.op[i] = *(const v4i*)(ap + s2_slot_off((i << S) + lr / kRows));
 #pragma unroll
   for (int k = 0; k < kS2KB; ++k) R.sw[k] = w2_scale[((size_t)j.e * kNHBlk + n0 / kBlk) * kNIBlk + kb0 + k];
 }
@@ -127,39 +123,36 @@ __device__ __forceinline__ v4i row_shl(const v4i& x) {
   }
 }
 
-// Operand slot C of a landed job in the MFMA layout (lane (q, r): row r); kFew:
-// slot C sits in op[C / 4], lanes shifted by 4 (C % 4).  Template constants:
-// a shift chosen at run time (folded only after unrolling) left the operands
-// in scratch memory.
-template <bool kFew, int C>
+// Operand slot C of a landed job in the MFMA layout (lane (q, r): row r);
+// spread S: slot C sits in op[C / 2^S], lanes shifted by (C mod 2^S) * 16 /
+// 2^S.  Template constants: a shift chosen at run time (folded only after
+// unrolling) left the operands in scratch memory.
+template <int S, int C>
 __device__ __forceinline__ v4i s2_operand(const S2Regs& R) {
-  if constexpr (kFew)
-    return row_shl<4 * (C % 4)>(R.op[C / 4]);
-  else
-    return R.op[C];
+  return row_shl<(C & ((1 << S) - 1)) * (16 >> S)>(R.op[C >> S]);
 }
 
 // s2_operand for the unrolled (k, g, h, part) of the MFMA loop: the 16 slot
 // constants spelled out, so that every shift is a template constant.
-template <bool kFew>
+template <int S>
 __device__ __forceinline__ v4i s2_op(const S2Regs& R, int k, int g, int h, int part) {
   switch (s2_slot(k, g, h, part)) {
-    case 0: return s2_operand<kFew, 0>(R);
-    case 1: return s2_operand<kFew, 1>(R);
-    case 2: return s2_operand<kFew, 2>(R);
-    case 3: return s2_operand<kFew, 3>(R);
-    case 4: return s2_operand<kFew, 4>(R);
-    case 5: return s2_operand<kFew, 5>(R);
-    case 6: return s2_operand<kFew, 6>(R);
-    case 7: return s2_operand<kFew, 7>(R);
-    case 8: return s2_operand<kFew, 8>(R);
-    case 9: return s2_operand<kFew, 9>(R);
-    case 10: return s2_operand<kFew, 10>(R);
-    case 11: return s2_operand<kFew, 11>(R);
-    case 12: return s2_operand<kFew, 12>(R);
-    case 13: return s2_operand<kFew, 13>(R);
-    case 14: return s2_operand<kFew, 14>(R);
-    default: return s2_operand<kFew, 15>(R);
+    case 0: return s2_operand<S, 0>(R);
+    case 1: return s2_operand<S, 1>(R);
+    case 2: return s2_operand<S, 2>(R);
+    case 3: return s2_operand<S, 3>(R);
+    case 4: return s2_operand<S, 4>(R);
+    case 5: return s2_operand<S, 5>(R);
+    case 6: return s2_operand<S, 6>(R);
+    case 7: return s2_operand<S, 7>(R);
+    case 8: return s2_operand<S, 8>(R);
+    case 9: return s2_operand<S, 9>(R);
+    case 10: return s2_operand<S, 10>(R);
+    case 11: return s2_operand<S, 11>(R);
+    case 12: return s2_operand<S, 12>(R);
+    case 13: return s2_operand<S, 13>(R);
+    case 14: return s2_operand<S, 14>(R);
+    default: return s2_operand<S, 15>(R);
   }
 }
 
@@ -223,17 +216,17 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
   // and so waited for the prefetch it had just issued, one full memory
   // latency per job (small_t64: 3.6 us per job, 2.1 of it that wait).
   // Every expert of the launch has at most four rows (every launch at T <= 4,
-  // decode among them): act rows spread over 4 loads per job (s2_load),
-  // one loop for the whole launch (decode_t1_s3 23.7 -> 22.6 us, T = 17
-  // 84.8 -> 79.0 us, same bits).
-  const bool few = __ballot(X.cnt > 4) == 0;
-  auto run = [&](auto few_c) {
-    constexpr bool kFew = decltype(few_c)::value;
+  // decode among them) or at most eight: act rows spread over 4 or 8 loads
+  // per job (s2_load), one loop for the whole launch (decode_t1_s3 23.7 ->
+  // 22.6 us, T = 17 84.8 -> 79.0 us, same bits).
+  const int spread = __ballot(X.cnt > 4) == 0 ? 2 : __ballot(X.cnt > 8) == 0 ? 1 : 0;
+  auto run = [&](auto spread_c) {
+    constexpr int S = decltype(spread_c)::value;
     S2Job job = s2_next(X, active, {-1, 0});
     S2Job j1 = job.e >= 0 ? s2_next(X, active, job) : job;
     S2Regs r0, r1;
     if (job.e >= 0) {
-      s2_load<kFew>(r0, job, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
+      s2_load<S>(r0, job, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
       s2_copy_w(stage(0), job, w2, n0, kb0, lane);
       s2_copy_w(stage(1), j1.e >= 0 ? j1 : job, w2, n0, kb0, lane);
     }
@@ -266,10 +259,10 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
           for (int g = 0; g < 2; ++g) {
             const v8bf b0 = e4m3x8_to_bf16((uint32_t)b[nb][k][g][0], (uint32_t)b[nb][k][g][1]);
             const v8bf b1 = e4m3x8_to_bf16((uint32_t)b[nb][k][g][2], (uint32_t)b[nb][k][g][3]);
-            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<kFew>(cur, k, g, 0, 0)), b0, p);
-            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<kFew>(cur, k, g, 1, 0)), b1, p);
-            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<kFew>(cur, k, g, 0, 1)), b0, p);
-            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<kFew>(cur, k, g, 1, 1)), b1, p);
+            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<S>(cur, k, g, 0, 0)), b0, p);
+            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<S>(cur, k, g, 1, 0)), b1, p);
+            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<S>(cur, k, g, 0, 1)), b0, p);
+            p = mfma_bf16_16x16x32(__builtin_bit_cast(v8bf, s2_op<S>(cur, k, g, 1, 1)), b1, p);
           }
   #pragma unroll
           for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(p[i], cur.sw[k], acc[i]);
@@ -281,7 +274,7 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
       // queue full their issue stalls, and the MFMAs no longer wait behind it
       // (small_t64 GEMM2 62.5 -> 61.5 us).
       if (j1.e >= 0) {
-        s2_load<kFew>(nxt, j1, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
+        s2_load<S>(nxt, j1, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
         s2_copy_w(stage(s), j2.e >= 0 ? j2 : j1, w2, n0, kb0, lane);
       }
       lds_barrier();
@@ -310,10 +303,12 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
       step(1, r1, r0);
     }
   };
-  if (few)
-    run(std::true_type{});
+  if (spread == 2)
+    run(std::integral_constant<int, 2>{});
+  else if (spread == 1)
+    run(std::integral_constant<int, 1>{});
   else
-    run(std::false_type{});
+    run(std::integral_constant<int, 0>{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the repeated copy lands before the LDS is released
   for (int i = threadIdx.x; i < T * kS2Cols; i += kS2Threads)
     out[(size_t)(i / kS2Cols) * kH + n0 + (i % kS2Cols)] = f32_to_bf16_rne(outacc[i]);

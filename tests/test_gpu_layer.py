@@ -47,9 +47,11 @@ LAYER_CASES = [
     # token counts on either side of each kernel-choice boundary
     ("small_t64", None, 17, None),        # first T past the in-GEMM1 routing
     # the hot experts take every token: experts of exactly 4 rows (act rows
-    # spread over 4 loads per GEMM2 job) and of 5 (16 loads)
+    # spread over 4 loads per GEMM2 job), of 5 and 8 (8 loads) and of 9 (16)
     ("skewed_t8192", None, 4, None),
     ("skewed_t8192", None, 5, None),
+    ("skewed_t8192", None, 8, None),
+    ("skewed_t8192", None, 9, None),
     ("small_t64", None, 24, None),        # largest T of the one-workgroup routing launch
     ("small_t64", None, 25, None),        # routing plus a permutation launch
     # streaming kernels with experts of more than 16 rows (four hot experts of
