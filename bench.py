@@ -193,8 +193,8 @@ def stage_times(pkg, torch, wl, iters):
 def near_tie_count(torch, logits, bias, ulps=8):
     """Tokens whose selection boundary (4th vs 5th group score, 8th vs 9th
     expert score among the kept groups) lies within `ulps` fp32 ulps: there
-    the expert ids may legitimately differ from the reference's (BASELINE.md
-    asks for the count).  fp32 torch on the inputs' device."""
+    the expert ids may legitimately differ from the reference's, so the bench
+    line reports the count.  fp32 torch on the inputs' device."""
     x = logits.float()
     s = 1.0 / (1.0 + torch.exp(-x))
     sb = s + bias.float().reshape(1, -1)
