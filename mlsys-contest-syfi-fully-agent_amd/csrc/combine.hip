@@ -16,20 +16,27 @@
 namespace moe {
 namespace {
 
-// 896 threads x 8 columns = one 7168-column row per workgroup; every lane
-// issues its (up to 8 rows x 2) 16-byte loads of fp32 GEMM2 rows before the
-// first add.  Thread i takes columns 4i .. 4i+3 and 3584 + 4i .. +3, so each
-// load instruction of a wave covers 1 KB of contiguous bytes.  The rows are
-// read once, with nontemporal loads (at T = 8192: 201 -> 183 us).
-constexpr int kCombThreads = 896;
-constexpr int kCombHalf = kH / 2;
-static_assert(kCombThreads * 4 == kCombHalf, "one row per workgroup");
+// A workgroup of kCombThreads threads combines kCombCols columns of one
+// token: thread i takes columns 4i .. 4i+3 and kCombCols / 2 + 4i .. +3 of
+// its part, so each load instruction of a wave covers 1 KB of contiguous
+// bytes, and every lane issues its (up to 8 rows x 2) 16-byte loads of fp32
+// GEMM2 rows before the first add.  The rows are read once, with
+// nontemporal loads (at T = 8192: 201 -> 183 us).  One wave per workgroup,
+// 14 per token: many small workgroups per CU overlap their index loads with
+// other tokens' row loads (interleaved runs, T = 4096 / 8192 / 14107: 93.2 /
+// 183.3 / 318.7 us with one 896-thread workgroup per token, 89.9 / 179.0 /
+// 311.5 with 64 threads; 448 and 128 threads in between; same bits).
+constexpr int kCombThreads = 64;
+constexpr int kCombCols = 8 * kCombThreads;
+constexpr int kCombParts = kH / kCombCols;  // workgroups per token
+static_assert(kCombParts * kCombCols == kH && kCombThreads % kWave == 0, "whole waves, whole parts");
 
 __global__ void __launch_bounds__(kCombThreads)
 combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_row,
                const float* __restrict__ topk_w, uint16_t* __restrict__ out) {
-  const int t = blockIdx.x;
-  const int c[2] = {(int)threadIdx.x * 4, kCombHalf + (int)threadIdx.x * 4};
+  const int t = blockIdx.x / kCombParts;
+  const int c0 = (blockIdx.x % kCombParts) * kCombCols + (int)threadIdx.x * 4;
+  const int c[2] = {c0, c0 + kCombCols / 2};
   int row[kTopK];
   float w[kTopK];
 #pragma unroll
@@ -68,7 +75,7 @@ combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_
 }  // namespace
 
 hipError_t launch_combine(int T, const Layout& L, char* ws, void* out, hipStream_t stream) {
-  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(kCombThreads), 0, stream,
+  hipLaunchKernelGGL(combine_kernel, dim3(T * kCombParts), dim3(kCombThreads), 0, stream,
                      (const float*)(ws + L.down), (const int32_t*)(ws + L.pair_row),
                      (const float*)(ws + L.topk_w), (uint16_t*)out);
   return hipGetLastError();
