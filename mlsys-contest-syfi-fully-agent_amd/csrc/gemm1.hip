@@ -440,7 +440,7 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
   if (t < 0) break;
   if (it > 0) block_barrier();  // every wave is done with the previous tile's LDS
   int mt, nt;
-  grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
+  grouped_tile(X, t, C::BM, C::kNT, C::kGroupM, mt, nt);
   int e, row0, rows;
   X.find_tile(mt, C::BM, e, row0, rows);
   const int j0 = nt * C::kGateCols;
@@ -671,7 +671,7 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
   const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
   if (t < 0) return;
   int mt, nt;
-  grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
+  grouped_tile(X, t, C::BM, C::kNT, C::kGroupM, mt, nt);
   int e, row0, rows;
   X.find_tile(mt, C::BM, e, row0, rows);
   const int j0 = nt * C::kGateCols;

@@ -383,7 +383,7 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
   const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
   if (t < 0) return;
   int mt, nt;
-  grouped_tile(t, mt_total, C::kNT, C::kGroupM, mt, nt);
+  grouped_tile(X, t, C::BM, C::kNT, C::kGroupM, mt, nt);
   int e, row0, rows;
   X.find_tile(mt, C::BM, e, row0, rows);
   const int n0 = nt * C::BN;

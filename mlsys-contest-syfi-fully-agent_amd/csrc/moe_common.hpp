@@ -383,18 +383,6 @@ __device__ __forceinline__ int xcd_tile_nth(int b, int G, int R, int i) {
   return (l < per && t < R) ? t : -1;
 }
 
-// Tile order inside the run: groups of `gm` row tiles sweep all `nt` column
-// tiles, row tile fastest, so concurrently running blocks reuse both the A
-// rows and the B columns of their group.
-__device__ __forceinline__ void grouped_tile(int t, int mt_total, int nt, int gm, int& mt, int& ntile) {
-  const int group = t / (gm * nt);
-  const int first = group * gm;
-  const int rows_in_group = min(gm, mt_total - first);
-  const int r = t - first * nt;
-  mt = first + r % rows_in_group;
-  ntile = r / rows_in_group;
-}
-
 // The 33 expert row offsets spread over the lanes of a wave (lane x holds
 // off[x], lanes past 32 hold off[32]), read with one vector load.  Every query
 // is wave-level (ballot / readlane / lane scan): all 64 lanes of the wave must
@@ -434,6 +422,19 @@ struct ExpertRows {
   __device__ __forceinline__ int count_tiles(int bm) const {
     return __builtin_amdgcn_readlane(tiles_incl(bm), kELocal - 1);
   }
+  // The L2 group of global row tile `tile` (< count_tiles(bm)): the run of at
+  // most gm row tiles of one expert that holds it; each expert's runs start
+  // at its first row tile.
+  __device__ __forceinline__ void tile_group(int tile, int bm, int gm, int& first, int& size) const {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int incl = tiles_incl(bm);
+    const uint64_t m = __ballot(lane < kELocal && incl > tile);
+    const int e = m ? __builtin_ctzll(m) : kELocal - 1;
+    const int e_end = __builtin_amdgcn_readlane(incl, e);
+    const int e_begin = e_end - __builtin_amdgcn_readlane((cnt + bm - 1) / bm, e);
+    first = e_begin + (tile - e_begin) / gm * gm;
+    size = min(gm, e_end - first);
+  }
   // Global row tile `tile` -> (expert, first row, rows in tile); false past the
   // last tile.
   __device__ __forceinline__ bool find_tile(int tile, int bm, int& e, int& row0, int& rows) const {
@@ -449,5 +450,19 @@ struct ExpertRows {
     return true;
   }
 };
+
+// Tile order inside the run: each L2 group (ExpertRows::tile_group) sweeps
+// all `nt` column tiles, row tile fastest, so concurrently running blocks
+// reuse the weight columns of their expert and the rows of their row tile.
+// A group covers tiles [first * nt, (first + size) * nt), so the row tile
+// t / nt lies in the group of tile t.
+__device__ __forceinline__ void grouped_tile(const ExpertRows& X, int t, int bm, int nt, int gm, int& mt,
+                                             int& ntile) {
+  int first, size;
+  X.tile_group(t / nt, bm, gm, first, size);
+  const int r = t - first * nt;
+  mt = first + r % size;
+  ntile = r / size;
+}
 
 }  // namespace moe
