@@ -413,7 +413,7 @@ struct G1Tiled {
   static constexpr int kScaleRowsPerWave = BM / kWaves;
   static_assert(kScaleRowsPerWave % 4 == 0 && kScaleRowsPerWave <= kWave, "scale rows per wave");
   static constexpr int kDmaPerStage = kPlanesPerWave + 1;
-  static constexpr int kGroupM = 4;             // row tiles per L2 group
+  static constexpr int kGroupM = 4;             // at most this many row tiles (of one expert) per L2 group
 };
 
 template <int WM, int WN, int MI>
