@@ -10,6 +10,8 @@ so import it with importlib:
     pkg.run(...)
 """
 from . import _lib, synth, verdict, workloads  # noqa: F401
-from .moe import intermediates, quantize_hidden, route, run, run_noalloc, workspace  # noqa: F401
+from .moe import (intermediates, quantize_hidden, release_workspaces, route, run, run_noalloc,  # noqa: F401
+                  workspace)
 
-__all__ = ["run", "run_noalloc", "route", "intermediates", "workspace", "quantize_hidden", "synth", "workloads", "verdict"]
+__all__ = ["run", "run_noalloc", "route", "intermediates", "workspace", "release_workspaces", "quantize_hidden", "synth",
+           "workloads", "verdict"]

@@ -96,7 +96,8 @@ def bench_lib() -> ctypes.CDLL:
         P = ctypes.c_void_p
         L.moe_bench_read_stream.argtypes = [P, ctypes.c_size_t, P, ctypes.c_int, P]
         L.moe_bench_mfma_loop.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P]
-        L.moe_bench_read_stream.restype = L.moe_bench_mfma_loop.restype = ctypes.c_int
+        L.moe_bench_trace_mark.argtypes = [ctypes.c_int, P]
+        L.moe_bench_read_stream.restype = L.moe_bench_mfma_loop.restype = L.moe_bench_trace_mark.restype = ctypes.c_int
         _bench = L
     return _bench
 

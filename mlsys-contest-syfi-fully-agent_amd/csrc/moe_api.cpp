@@ -185,7 +185,10 @@ int moe_fp8_ds_run_noalloc(const float* routing_logits, const void* routing_bias
                            const float* gemm1_weights_scale, const void* gemm2_weights,
                            const float* gemm2_weights_scale, int64_t local_expert_offset,
                            double routed_scaling_factor, void* output, int64_t T, hipStream_t stream) {
-  if (T < 0) return MOE_FP8_DS_ERR_SHAPE;
+  // the order of check_common, so that both entry points return the same
+  // status for the same bad argument; the scratch limit comes after them
+  if (T < 0 || T > moe::kMaxTokens) return MOE_FP8_DS_ERR_SHAPE;
+  if (!std::isfinite(routed_scaling_factor)) return MOE_FP8_DS_ERR_ARG;
   if (T > MOE_FP8_DS_NOALLOC_MAX_TOKENS) return MOE_FP8_DS_ERR_SCRATCH;
   if (T == 0) return MOE_FP8_DS_OK;
   void* ws = noalloc_scratch();

@@ -5,7 +5,9 @@
 //     (what the layer's HBM-bound kernels do with the expert weights);
 //   * MFMA issue rate: independent accumulator chains of the two instructions
 //     the GEMMs use (v_mfma_f32_16x16x128_f8f6f4 and v_mfma_f32_16x16x32_bf16),
-//     operands in registers, launched by bench.py at 16 waves per CU.
+//     operands in registers, launched by bench.py at 16 waves per CU;
+//   * trace markers: two empty kernels whose dispatches split a kernel trace
+//     of several workloads' calls into per-workload spans.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -76,6 +78,9 @@ __global__ void __launch_bounds__(512) mfma_bf16_loop(int iters, float* __restri
   sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+__global__ void trace_mark_begin() {}
+__global__ void trace_mark_end() {}
+
 }  // namespace
 
 extern "C" {
@@ -97,6 +102,16 @@ int moe_bench_mfma_loop(int kind, int iters, int blocks, void* sink, hipStream_t
     hipLaunchKernelGGL(mfma_f8_loop, dim3(blocks), dim3(512), 0, stream, iters, (float*)sink);
   else
     hipLaunchKernelGGL(mfma_bf16_loop, dim3(blocks), dim3(512), 0, stream, iters, (float*)sink);
+  return (int)hipGetLastError();
+}
+
+// Dispatches the empty kernel trace_mark_begin (end = 0) or trace_mark_end
+// (end != 0) on `stream`.  Returns a hipError_t.
+int moe_bench_trace_mark(int end, hipStream_t stream) {
+  if (end)
+    hipLaunchKernelGGL(trace_mark_end, dim3(1), dim3(64), 0, stream);
+  else
+    hipLaunchKernelGGL(trace_mark_begin, dim3(1), dim3(64), 0, stream);
   return (int)hipGetLastError();
 }
 

@@ -19,6 +19,7 @@ only checks arguments, owns a workspace per (device, stream) and passes pointers
 from __future__ import annotations
 
 import threading
+from collections import OrderedDict
 
 import torch
 
@@ -36,7 +37,16 @@ FUSED_COMBINE_MAX_TOKENS = 64
 ROUTE_ONE_WORKGROUP_MAX_TOKENS = 24
 
 _ws_lock = threading.Lock()
-_ws: dict = {}
+# Workspaces by (device type, device index, stream), least recently used
+# first.  At most WORKSPACE_CACHE_ENTRIES are kept: code that makes a stream
+# per request no longer piles up one workspace per stream (about 2.4 GB each
+# at T = 8192).
+WORKSPACE_CACHE_ENTRIES = 8
+_ws: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+# Buffers handed out while the stream was being captured into a graph: the
+# graph writes into them on every replay, so they stay alive when the cache
+# drops or outgrows them, until release_workspaces().
+_ws_captured: list = []
 
 _F8, _F32, _BF16 = torch.float8_e4m3fn, torch.float32, torch.bfloat16
 # torch's raw-pointer accessor of the current stream (what
@@ -58,15 +68,32 @@ def workspace(device: torch.device, T: int, stream: int | None = None) -> torch.
     streams never share one (the C entry points need distinct workspaces for
     concurrent calls), and a buffer is allocated on the stream that uses it,
     so when it grows, torch's caching allocator hands the old memory out
-    again only to later work on that same stream."""
+    again only to later work on that same stream.  The cache keeps the
+    WORKSPACE_CACHE_ENTRIES most recently used streams' buffers; a buffer
+    handed out during graph capture is also kept for the graph's replays
+    (see release_workspaces)."""
     need = _lib.moe_lib().moe_fp8_ds_workspace_size(T)
     key = (device.type, device.index, _stream(device) if stream is None else stream)
+    capturing = device.type == "cuda" and torch.cuda.is_current_stream_capturing()
     with _ws_lock:
         buf = _ws.get(key)
         if buf is None or buf.numel() < need:
             buf = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=device)
             _ws[key] = buf
+        _ws.move_to_end(key)
+        if capturing and not any(b is buf for b in _ws_captured):
+            _ws_captured.append(buf)
+        while len(_ws) > WORKSPACE_CACHE_ENTRIES:
+            _ws.popitem(last=False)
         return buf
+
+
+def release_workspaces() -> None:
+    """Drops every cached workspace, including those kept for captured graphs:
+    call it only once no graph that ran the layer will be replayed again."""
+    with _ws_lock:
+        _ws.clear()
+        _ws_captured.clear()
 
 
 def _ptr(t: torch.Tensor) -> int:

@@ -85,6 +85,15 @@ def test_noalloc_validation_without_gpu(pkg):
     assert L.moe_fp8_ds_run_noalloc(p, p, p, p, p, p, p, p, 0, 2.5, p, lim + 1, None) == pkg._lib.ERR_SCRATCH
     assert L.moe_fp8_ds_run_noalloc(p, p, p, p, p, p, p, p, 0, 2.5, p, -1, None) == -2
     assert L.moe_fp8_ds_run_noalloc(p, p, p, p, p, p, p, p, 0, 2.5, p, 0, None) == 0
+    # the same status as moe_fp8_ds_run for the same bad argument, checked in
+    # the same order, before the scratch limit and the T == 0 no-op
+    big = L.moe_fp8_ds_max_tokens() + 1
+    assert L.moe_fp8_ds_run_noalloc(p, p, p, p, p, p, p, p, 0, 2.5, p, big, None) == -2
+    assert _run(L, p, big, p, 1 << 40) == -2
+    for rsf in (float("nan"), float("inf")):
+        for T in (0, 4, lim + 1):
+            assert L.moe_fp8_ds_run_noalloc(p, p, p, p, p, p, p, p, 0, rsf, p, T, None) == -6, (rsf, T)
+            assert _run(L, p, T, p, 1 << 40, rsf=rsf) == -6, (rsf, T)
     # the header's limit is what the library enforces
     hdr = open(os.path.join(ROOT, "include", "moe_fp8_ds.h")).read()
     assert re.search(r"#define MOE_FP8_DS_NOALLOC_MAX_TOKENS (\d+)", hdr).group(1) == str(lim)

@@ -65,8 +65,8 @@ LAYER_CASES = [
     ("skewed_t8192", None, 2048, None),
     ("skewed_t8192", None, 4095, None),
     ("skewed_t8192", None, 4096, None),
-    # the contest dataset's largest T (moe.py:13), sampled
-    ("skewed_t8192", None, 14107, 768),
+    # the contest dataset's largest T (moe.py:13), every token
+    ("skewed_t8192", None, 14107, None),
 ]
 
 

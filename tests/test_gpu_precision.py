@@ -8,10 +8,16 @@ intermediates (act, GEMM2 rows) then fail several percent of the elements.
 The layer carries act as a bf16 (hi, lo) pair and the GEMM2 rows in fp32.
 Outputs are scaled up through hidden_states_scale (the layer is linear in
 it up to SwiGLU, so outputs grow about as its square) and checked against
-the oracle with the verdict driver's check in match-ratio mode, at the
-fraction the reference's CUDA notes record for the harness
-(moe/solution/cuda/moe.cu:1802: 0.998).  The allclose verdict is printed
-beside it.  It cannot be required: GEMM1 runs on the fp8 MFMA, whose block
+the oracle with the verdict driver's check.  Two bars, both this project's
+own (no harness rule pins a match ratio: the reference's runner checks with
+rtol = 100, atol = 1e10, moe/scripts/run_local.py:33, and the 0.998 of
+moe/solution/cuda/moe.cu:1802 is one variant's observed ratio, not a rule):
+  * the match-ratio verdict at 0.998, the looser bar a caller may apply;
+  * a regression floor per factor close to the measured matched fraction
+    (x30: 0.99996, 33 of 917,504 elements outside; x300: 0.99926), so any
+    change that loses precision fails here.
+The strict allclose verdict and its failure count are printed.  It cannot be
+required: GEMM1 runs on the fp8 MFMA, whose block
 sums carry ~2^-15 rms error (tests/test_gpu_mfma_precision.py), so at these
 magnitudes a few elements in 10^5 that cancel to near zero exceed 1%.  The
 torch fp32 restatement of the definition on the GPU (verdict.reference_layer,
@@ -28,7 +34,12 @@ pytestmark = pytest.mark.gpu
 H = 7168
 
 
-HARNESS_MATCH_RATIO = 0.998  # moe/solution/cuda/moe.cu:1802
+# This project's own match-ratio bar (0.998 is the ratio one reference
+# variant recorded, moe/solution/cuda/moe.cu:1802; no harness rule pins it).
+MATCH_RATIO_BAR = 0.998
+# Regression floors: the measured matched fractions (x30 0.999964, x300
+# 0.999259) less a margin of a few elements in 10^5.
+MATCHED_FLOOR = {30.0: 0.99990, 300.0: 0.99900}
 
 
 @pytest.mark.parametrize("factor", [30.0, 300.0])
@@ -49,12 +60,15 @@ def test_large_magnitude_output(pkg, orc, cuda_device, factor):
     ref = torch.from_numpy(ref_bits.view(np.int16)).view(torch.bfloat16).to(cuda_device)
     v = pkg.verdict
     chk_all = v.check_output(out, ref)
-    chk_ratio = v.check_output(out, ref, required_matched_ratio=HARNESS_MATCH_RATIO)
+    chk_ratio = v.check_output(out, ref, required_matched_ratio=MATCH_RATIO_BAR)
     floor = v.check_output(v.reference_layer(*tok, *w, cfg.local_expert_offset, cfg.routed_scaling_factor), ref)
     mag = ref.float().abs()
+    n = out.numel()
+    fails = int(round((1.0 - chk_all.matched_ratio) * n))
     print(f"  max|ref| {mag.max().item():.4g}, median|ref| {mag.median().item():.4g}; "
-          f"layer: matched {chk_all.matched_ratio:.6f} ({chk_all.status} allclose, {chk_ratio.status} at "
-          f"{HARNESS_MATCH_RATIO}), "
+          f"layer: matched {chk_all.matched_ratio:.6f}, strict allclose {chk_all.status} "
+          f"({fails} of {n} elements outside atol=rtol=1e-2), {chk_ratio.status} at {MATCH_RATIO_BAR}, "
           f"max|err| {chk_all.max_abs_err:.4g}; torch fp32 floor: matched {floor.matched_ratio:.6f} ({floor.status})")
     assert mag.max().item() > 10 * factor  # the scaling did reach large magnitudes
     assert chk_ratio.status == v.PASSED
+    assert chk_all.matched_ratio >= MATCHED_FLOOR[factor], (chk_all.matched_ratio, MATCHED_FLOOR[factor])

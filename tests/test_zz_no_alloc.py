@@ -65,3 +65,62 @@ def test_noalloc_rejects_large_T(pkg, cuda_device):
     assert (out == 0).all()  # nothing was launched
     empty = [t[:0] for t in tok]
     assert _call_noalloc(pkg, empty, w, 0, 2.5, out[:0]) == 0
+
+
+# Run in a fresh process: its first moe_fp8_ds_run_noalloc call (which looks
+# up the device's scratch address) happens inside a graph capture.
+_CAPTURE_SCRIPT = r"""
+import ctypes, importlib, sys
+import torch
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[1] + "/tests")
+from util import gpu_tokens, gpu_weights
+pkg = importlib.import_module("mlsys-contest-syfi-fully-agent_amd")
+dev = torch.device("cuda:0")
+cfg = pkg.synth.CONFIGS["small_t64"]
+w, _ = gpu_weights(pkg, cfg.seed, dev)
+tok, _ = gpu_tokens(pkg, cfg, dev, 48)
+T = 48
+got = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+torch.cuda.synchronize()
+# no kernel of the layer's library has run in this process before the capture
+s = torch.cuda.Stream(device=dev)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=s):
+    pkg.run_noalloc(*tok, *w, cfg.local_expert_offset, cfg.routed_scaling_factor, got)
+torch.cuda.synchronize()
+ref = torch.full((T, 7168), float("nan"), dtype=torch.bfloat16, device=dev)
+pkg.run(*tok, *w, cfg.local_expert_offset, cfg.routed_scaling_factor, ref)
+torch.cuda.synchronize()
+other, _ = gpu_tokens(pkg, cfg, dev, 20)
+other_out = torch.empty((20, 7168), dtype=torch.bfloat16, device=dev)
+for rep in range(3):
+    got.fill_(float("nan"))
+    # eager work between replays: an eager no-alloc call that overwrites the
+    # shared scratch with another input's intermediates
+    pkg.run_noalloc(*other, *w, cfg.local_expert_offset, cfg.routed_scaling_factor, other_out)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    ok = torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    print(f"noalloc captured first call: replay {rep} {'equal' if ok else 'DIFFERS'}", flush=True)
+    if not ok:
+        sys.exit(1)
+print("noalloc capture ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture(cuda_device):
+    """The first no-allocation call of a process, and its first call into the
+    layer's library at all, is made inside a graph capture; every replay (with eager no-alloc calls on other inputs in
+    between) equals moe_fp8_ds_run's bits."""
+    import os
+    import subprocess
+    import sys
+
+    from conftest import ROOT
+
+    print("noalloc capture case: fresh process, T=48", flush=True)
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, ROOT], capture_output=True, text=True, timeout=110,
+                       env=dict(os.environ))
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "noalloc capture ok" in r.stdout
