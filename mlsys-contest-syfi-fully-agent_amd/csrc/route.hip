@@ -42,6 +42,13 @@ constexpr int kRouteSingleMaxTokens = 24;
 constexpr int kRouteWavesMulti = 4;  // tokens per route workgroup, 24 < T <= kRouteMultiSmallMaxTokens
 constexpr int kRouteMultiSmallMaxTokens = 1024;
 constexpr int kRouteThreads = kRouteWaves * kWave;
+// Waves per permutation workgroup for 64 < T <= kRouteMultiSmallMaxTokens
+// (128 tokens each, so T = 1024 takes 8 workgroups) and beyond (256 tokens
+// each, 32 workgroups at T = 8192).
+constexpr int kPermWavesMid = 2;
+constexpr int kPermWavesLarge = 4;
+static_assert((kPermWavesMid * kWave) % kRouteWavesMulti == 0, "a chunk covers whole route workgroups");
+static_assert((kPermWavesLarge * kWave) % kRouteWaves == 0, "a chunk covers whole route workgroups");
 
 // Local-expert bitmask of a token's 8 ascending ids, and the slot of its first
 // local id (ids ascending => local ids occupy slots kfirst .. kfirst+popc-1).
@@ -62,6 +69,7 @@ __device__ __forceinline__ uint32_t local_mask(const int32_t id[kTopK], int64_t 
 // Shared memory of the permutation pass, for a workgroup of kPW waves.
 template <int kPW>
 struct PermShared {
+  uint64_t wave_bal[kPW][kELocal];  // per wave and expert: ballot of the lanes (tokens) that pick it
   int wave_cnt[kPW][kELocal];
   int wave_base[kPW][kELocal];
   int running[kELocal];  // next free row per expert
@@ -110,29 +118,35 @@ __device__ __forceinline__ TokenPicks load_picks(const int32_t* __restrict__ ids
 }
 
 // Rows of the pairs of tokens [t0, t0 + 64 kPW): ascending token order inside
-// each expert, starting at sh.running[e].  Every thread takes part.
+// each expert, starting at sh.running[e].  Every thread takes part.  Each
+// wave takes its 32 per-expert ballots once (lane e keeps expert e's), then
+// every lane ranks only its own local picks against them (mbcnt): a loop
+// over all 32 experts per pick, with the row slot chosen at run time, made
+// ~2,700 instructions of one wave's serial work (T = 64: 6.5 us).
 template <int kPW>
 __device__ void scatter_chunk(const TokenPicks& pk, int T, int t0, int64_t offset, PermShared<kPW>& sh,
                               int32_t* __restrict__ pair_row, int32_t* __restrict__ perm_token,
                               float* __restrict__ perm_w) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int t = t0 + threadIdx.x;
+  const int32_t id[kTopK] = {pk.a.x, pk.a.y, pk.a.z, pk.a.w, pk.b.x, pk.b.y, pk.b.z, pk.b.w};
   int kf = kTopK;
   uint32_t m = 0;  // tokens past T have no local expert
-  if (t < T) {
-    const int32_t id[kTopK] = {pk.a.x, pk.a.y, pk.a.z, pk.a.w, pk.b.x, pk.b.y, pk.b.z, pk.b.w};
-    m = local_mask(id, offset, kf);
-  }
-  // per-expert counts of this wave: lane le keeps popc(ballot of expert le)
-  int mycnt = 0;
+  if (t < T) m = local_mask(id, offset, kf);
+  // lane le receives expert le's ballot (v_writelane: the ballot is uniform)
+  int mine_lo = 0, mine_hi = 0;
 #pragma unroll
   for (int le = 0; le < kELocal; ++le) {
-    const int c = __popcll(__ballot((m >> le) & 1u));
-    if (lane == le) mycnt = c;
+    const uint64_t b = __ballot((m >> le) & 1u);
+    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(mine_lo) : "s"((uint32_t)b), "s"(le));
+    asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(mine_hi) : "s"((uint32_t)(b >> 32)), "s"(le));
   }
-  if (lane < kELocal) sh.wave_cnt[wave][lane] = mycnt;
+  const uint64_t mine = ((uint64_t)(uint32_t)mine_hi << 32) | (uint32_t)mine_lo;
+  if (lane < kELocal) {
+    sh.wave_bal[wave][lane] = mine;
+    sh.wave_cnt[wave][lane] = __popcll(mine);
+  }
   __syncthreads();
   if (threadIdx.x < kELocal) {
     int acc = sh.running[threadIdx.x];
@@ -144,19 +158,27 @@ __device__ void scatter_chunk(const TokenPicks& pk, int T, int t0, int64_t offse
     sh.running[threadIdx.x] = acc;
   }
   __syncthreads();
-  // Rows: the wave's base for the expert plus the lane's rank among the
-  // wave's lanes holding that expert (ballots again; every lane takes part).
+  // Row of pick k: the wave's base for its expert plus the number of lanes
+  // below this one holding that expert.
+  // (every pick reads the tables, at a clamped index, so that the 16 LDS
+  // reads go out together instead of one wait per pick)
   int32_t row[kTopK];
+  bool loc[kTopK];
+  uint64_t bal[kTopK];
+  int base[kTopK];
 #pragma unroll
-  for (int k = 0; k < kTopK; ++k) row[k] = -1;
-  int j = kf;
+  for (int k = 0; k < kTopK; ++k) {
+    const int64_t le = (int64_t)id[k] - offset;
+    loc[k] = t < T && le >= 0 && le < kELocal;
+    const int e = loc[k] ? (int)le : 0;
+    bal[k] = sh.wave_bal[wave][e];
+    base[k] = sh.wave_base[wave][e];
+  }
 #pragma unroll
-  for (int le = 0; le < kELocal; ++le) {
-    const uint64_t b = __ballot((m >> le) & 1u);
-    if ((m >> le) & 1u) {
-      row[j] = sh.wave_base[wave][le] + __popcll(b & lt_mask);
-      ++j;
-    }
+  for (int k = 0; k < kTopK; ++k) {
+    const int rank =
+        (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal[k] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal[k], 0u));
+    row[k] = loc[k] ? base[k] + rank : -1;
   }
   if (t < T) {
     int4 r0, r1;
@@ -221,45 +243,60 @@ route_kernel(const float* __restrict__ logits, const uint16_t* __restrict__ bias
   if (threadIdx.x < kELocal) block_hist[(size_t)blockIdx.x * kELocal + threadIdx.x] = hist[threadIdx.x];
 }
 
-// Permutation for T > 16: workgroup c of kPW waves handles tokens
+// Permutation for T > 24: workgroup c of kPW waves handles tokens
 // [64 kPW c, 64 kPW (c + 1)).  Every workgroup reduces the route histograms to
 // the per-expert totals and to the counts of the tokens before its chunk;
-// workgroup 0 writes expert_off.  T <= 64 takes one wave (kPW = 1): sixteen
-// waves spent ~4 us more on their per-expert ballot loops and barriers.
+// workgroup 0 writes expert_off.  The scatter's per-expert ballot loops are
+// serial per wave, so the chunk is kept small up to T = 1024 (two waves, up
+// to 8 workgroups: T = 1024 one 1024-thread workgroup took 8.9 us, 16 waves on
+// one CU) and T <= 64 takes one wave.
 template <int kPW>
 __global__ void __launch_bounds__(kPW * kWave)
 perm_kernel(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, int T, int64_t offset,
             const int32_t* __restrict__ block_hist, int tokens_per_block, int32_t* __restrict__ pair_row,
             int32_t* __restrict__ expert_off, int32_t* __restrict__ perm_token, float* __restrict__ perm_w) {
   constexpr int kThreads = kPW * kWave;
-  constexpr int kGroups = kThreads / kELocal;
   __shared__ PermShared<kPW> sh;
-  __shared__ int part_tot[kGroups][kELocal];
-  __shared__ int part_pre[kGroups][kELocal];
+  __shared__ int4 wave_tot[kPW][kELocal / 4];
+  __shared__ int4 wave_pre[kPW][kELocal / 4];
   const int nb = (T + tokens_per_block - 1) / tokens_per_block;
   const int first = blockIdx.x * (kThreads / tokens_per_block);  // route workgroups before this chunk
   const TokenPicks pk0 = load_picks(ids, topk_w, T, blockIdx.x * kThreads + threadIdx.x);
-  const int e = threadIdx.x % kELocal;
-  const int g = threadIdx.x / kELocal;
-  int tot = 0, pre = 0;
-  // eight histogram loads in flight per thread (one wait per batch, not per
-  // load: T = 1024 has 256 route histograms, 8 per thread), from clamped
-  // addresses so that no load sits under a branch
-  constexpr int kBatch = 8;
-  for (int b0 = g; b0 < nb; b0 += kBatch * kGroups) {
-    int v[kBatch];
+  // Histogram rows are 128 bytes: 8 threads per row, one int4 (experts
+  // 4 c4 .. 4 c4 + 3) each, kRows rows per round, kBatch loads in flight per
+  // thread (one wait per batch), from clamped addresses so that no load sits
+  // under a branch.
+  constexpr int kRows = kThreads / 8;
+  constexpr int kBatch = kRows >= 64 ? 4 : 16;
+  const int c4 = threadIdx.x & 7;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  int4 tot = {0, 0, 0, 0}, pre = {0, 0, 0, 0};
+  for (int b0 = threadIdx.x >> 3; b0 < nb; b0 += kBatch * kRows) {
+    int4 v[kBatch];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) v[i] = block_hist[(size_t)min(b0 + i * kGroups, nb - 1) * kELocal + e];
+    for (int i = 0; i < kBatch; ++i)
+      v[i] = *(const int4*)(block_hist + (size_t)min(b0 + i * kRows, nb - 1) * kELocal + 4 * c4);
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      const int b = b0 + i * kGroups;
-      const int x = b < nb ? v[i] : 0;
-      tot += x;
-      if (b < first) pre += x;
+    for (int i = 0; i < kBatch; ++i) {  // masks, not branches: rows past nb or at / after this chunk
+      const int b = b0 + i * kRows;
+      const int mt = -(int)(b < nb), mp = mt & -(int)(b < first);
+      tot.x += v[i].x & mt; tot.y += v[i].y & mt; tot.z += v[i].z & mt; tot.w += v[i].w & mt;
+      pre.x += v[i].x & mp; pre.y += v[i].y & mp; pre.z += v[i].z & mp; pre.w += v[i].w & mp;
     }
   }
-  part_tot[g][e] = tot;
-  part_pre[g][e] = pre;
+  // lanes l, l ^ 8, l ^ 16, ... hold the same four experts
+#pragma unroll
+  for (int m = 8; m < kWave; m <<= 1) {
+    tot.x += __shfl_xor(tot.x, m, kWave); tot.y += __shfl_xor(tot.y, m, kWave);
+    tot.z += __shfl_xor(tot.z, m, kWave); tot.w += __shfl_xor(tot.w, m, kWave);
+    pre.x += __shfl_xor(pre.x, m, kWave); pre.y += __shfl_xor(pre.y, m, kWave);
+    pre.z += __shfl_xor(pre.z, m, kWave); pre.w += __shfl_xor(pre.w, m, kWave);
+  }
+  if (lane < 8) {
+    wave_tot[wave][lane] = tot;
+    wave_pre[wave][lane] = pre;
+  }
   // the picks are first used only here, after the histogram loads went out
   // (the compiler would otherwise use them first and wait for them alone)
   TokenPicks pk = pk0;
@@ -271,9 +308,9 @@ perm_kernel(const int32_t* __restrict__ ids, const float* __restrict__ topk_w, i
   if (threadIdx.x < kELocal) {
     int a = 0, p = 0;
 #pragma unroll
-    for (int k = 0; k < kGroups; ++k) {
-      a += part_tot[k][threadIdx.x];
-      p += part_pre[k][threadIdx.x];
+    for (int w = 0; w < kPW; ++w) {
+      a += ((const int*)wave_tot[w])[threadIdx.x];
+      p += ((const int*)wave_pre[w])[threadIdx.x];
     }
     sh.total[threadIdx.x] = a;
     sh.before[threadIdx.x] = p;
@@ -311,10 +348,18 @@ hipError_t launch_route(const float* logits, const uint16_t* bias, float rsf, in
   if (T <= kWave) {
     hipLaunchKernelGGL(perm_kernel<1>, dim3(1), dim3(kWave), 0, stream, (const int32_t*)ids, (const float*)w, T,
                        offset, (const int32_t*)hist, tpb, pair_row, off, perm_token, perm_w);
+  } else if (T <= kRouteMultiSmallMaxTokens) {
+    constexpr int kPermThreadsMid = kPermWavesMid * kWave;
+    const int chunks = (T + kPermThreadsMid - 1) / kPermThreadsMid;
+    hipLaunchKernelGGL(perm_kernel<kPermWavesMid>, dim3(chunks), dim3(kPermThreadsMid), 0, stream,
+                       (const int32_t*)ids, (const float*)w, T, offset, (const int32_t*)hist, tpb, pair_row, off,
+                       perm_token, perm_w);
   } else {
-    const int chunks = (T + kRouteThreads - 1) / kRouteThreads;
-    hipLaunchKernelGGL(perm_kernel<kRouteWaves>, dim3(chunks), dim3(kRouteThreads), 0, stream, (const int32_t*)ids,
-                       (const float*)w, T, offset, (const int32_t*)hist, tpb, pair_row, off, perm_token, perm_w);
+    constexpr int kPermThreadsLarge = kPermWavesLarge * kWave;
+    const int chunks = (T + kPermThreadsLarge - 1) / kPermThreadsLarge;
+    hipLaunchKernelGGL(perm_kernel<kPermWavesLarge>, dim3(chunks), dim3(kPermThreadsLarge), 0, stream,
+                       (const int32_t*)ids, (const float*)w, T, offset, (const int32_t*)hist, tpb, pair_row, off,
+                       perm_token, perm_w);
   }
   return hipGetLastError();
 }

@@ -24,6 +24,12 @@ CASES = [
     ("prefill_t1024", None, 24),    # largest T of the one-workgroup routing
     ("prefill_t1024", None, 25),    # smallest T of routing plus a permutation launch
     ("skewed_t8192", 64, 777),      # ragged, large
+    # permutation workgroup shapes: one wave (T <= 64), 128-token chunks
+    # (64 < T <= 1024), 1024-token chunks beyond
+    ("prefill_t1024", None, 64),
+    ("prefill_t1024", None, 65),
+    ("prefill_t1024", None, 129),
+    ("skewed_t8192", None, 1025),
 ]
 
 
