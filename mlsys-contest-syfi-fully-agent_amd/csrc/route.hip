@@ -28,8 +28,6 @@
 //   * ranks inside a chunk come from wave ballots, so rows of an expert are in
 //     ascending token order and the result is deterministic; no host round
 //     trip at any T.
-#include <utility>
-
 #include "route_token.hpp"
 
 namespace moe {
@@ -119,21 +117,6 @@ __device__ __forceinline__ TokenPicks load_picks(const int32_t* __restrict__ ids
   return p;
 }
 
-// Lane le of (lo, hi) receives the ballot of bit le of m, for each le in LE
-// (v_writelane with the lane as an inline constant: a ballot is uniform, and
-// gfx950 allows one SGPR operand per instruction; a select per expert took
-// ~7 instructions instead of 2).
-template <int... LE>
-__device__ __forceinline__ void ballots_to_lanes(uint32_t m, int& lo, int& hi, std::integer_sequence<int, LE...>) {
-  (
-      [&] {
-        const uint64_t b = __ballot((m >> LE) & 1u);
-        asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(lo) : "s"((uint32_t)b), "n"(LE));
-        asm volatile("v_writelane_b32 %0, %1, %2" : "+v"(hi) : "s"((uint32_t)(b >> 32)), "n"(LE));
-      }(),
-      ...);
-}
-
 // Rows of the pairs of tokens [t0, t0 + 64 kPW): ascending token order inside
 // each expert, starting at sh.running[e].  Every thread takes part.  Each
 // wave takes its 32 per-expert ballots once (lane e keeps expert e's), then
@@ -151,9 +134,13 @@ __device__ void scatter_chunk(const TokenPicks& pk, int T, int t0, int64_t offse
   int kf = kTopK;
   uint32_t m = 0;  // tokens past T have no local expert
   if (t < T) m = local_mask(id, offset, kf);
-  int mine_lo = 0, mine_hi = 0;
-  ballots_to_lanes(m, mine_lo, mine_hi, std::make_integer_sequence<int, kELocal>{});
-  const uint64_t mine = ((uint64_t)(uint32_t)mine_hi << 32) | (uint32_t)mine_lo;
+  // lane le keeps expert le's ballot
+  uint64_t mine = 0;
+#pragma unroll
+  for (int le = 0; le < kELocal; ++le) {
+    const uint64_t b = __ballot((m >> le) & 1u);
+    if (lane == le) mine = b;
+  }
   if (lane < kELocal) {
     sh.wave_bal[wave][lane] = mine;
     sh.wave_cnt[wave][lane] = __popcll(mine);
