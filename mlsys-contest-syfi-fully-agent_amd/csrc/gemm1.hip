@@ -604,7 +604,8 @@ hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, c
   const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
   static ResidentGrid resident(gemm1_tiled_kernel<WM, WN, MI>, C::kThreads);
   const int64_t upper = ((mtiles * C::kNT + 7) / 8) * 8;
-  const int64_t cap = resident.n >= 8 ? resident.n / 8 * 8 : 8;
+  const int resident_n = resident.count();
+  const int64_t cap = resident_n >= 8 ? resident_n / 8 * 8 : 8;
   const int64_t blocks = upper < cap ? upper : cap;
   hipLaunchKernelGGL((gemm1_tiled_kernel<WM, WN, MI>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
                      stream, hs, hs_scale, T, w13, w13_scale, (const int32_t*)(ws + L.expert_off),
@@ -667,11 +668,15 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
 
   ExpertRows X;
   X.load(expert_off);
-  const int mt_total = X.count_tiles(C::BM);
-  const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
-  if (t < 0) return;
+  // An eighth of every expert's tiles per XCD (xcd_expert_tile): block b
+  // takes tiles b / 8, b / 8 + cap, ... of XCD b % 8 (one: an XCD holds at most
+  // 32 tiles more than an eighth of all, within the grid's margin).
+  const int xcd = blockIdx.x % 8, cap = gridDim.x / 8;
+#pragma unroll 1
+  for (int li = blockIdx.x / 8;; li += cap) {
   int mt, nt;
-  grouped_tile(X, t, C::BM, C::kNT, C::kGroupM, mt, nt);
+  if (!xcd_expert_tile(X, xcd, li, C::BM, C::kNT, C::kGroupM, mt, nt)) break;
+  if (li >= cap) block_barrier();  // every wave is done with the previous tile's LDS
   int e, row0, rows;
   X.find_tile(mt, C::BM, e, row0, rows);
   const int j0 = nt * C::kGateCols;
@@ -875,6 +880,7 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
         *(uint2*)(p + 64) = l;
       }
     }
+  }
   }
 }
 

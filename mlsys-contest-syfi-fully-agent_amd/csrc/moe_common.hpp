@@ -3,6 +3,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -348,21 +350,37 @@ __device__ __forceinline__ int xcd_tile(int b, int R) {
   return (b < per * 8 && t < R) ? t : -1;
 }
 
-// Workgroups of one kernel that fit on the device at once (compute units x
-// resident workgroups per CU), queried once, on first use.  A persistent
-// kernel launches min(work items, this) workgroups and strides over its items.
+// Workgroups of one kernel that fit on the current device at once (compute
+// units x resident workgroups per CU), queried on the first launch on each
+// device (a process may drive devices of different sizes).  A persistent
+// kernel launches min(work items, this) workgroups and strides over its
+// items.
 struct ResidentGrid {
-  int n = 0;
+  static constexpr int kMaxDevices = 64;
+  const void* kernel;
+  int threads;
+  size_t dyn_lds;
+  std::atomic<int> n[kMaxDevices] = {};
   template <typename Kernel>
-  ResidentGrid(Kernel kernel, int threads, size_t dyn_lds = 0) {
-    int dev = 0, cus = 0, per = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, dyn_lds) == hipSuccess)
-      n = cus * (per > 0 ? per : 1);
-    if (n <= 0) n = 256;
+  ResidentGrid(Kernel k, int t, size_t lds = 0) : kernel((const void*)k), threads(t), dyn_lds(lds) {}
+  int count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
+    int v = n[dev].load(std::memory_order_relaxed);
+    if (v <= 0) {
+      int cus = 0, per = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, dyn_lds) == hipSuccess)
+        v = cus * (per > 0 ? per : 1);
+      if (v <= 0) v = 256;
+      n[dev].store(v, std::memory_order_relaxed);  // every thread computes the same value
+    }
+    return v;
   }
-  int limit(int items) const { return items < n ? (items > 0 ? items : 1) : n; }
+  int limit(int items) {
+    const int c = count();
+    return items < c ? (items > 0 ? items : 1) : c;
+  }
 };
 
 // Index of the k-th set bit of m (k < popcount(m)).
@@ -463,6 +481,50 @@ __device__ __forceinline__ void grouped_tile(const ExpertRows& X, int t, int bm,
   const int r = t - first * nt;
   mt = first + r % size;
   ntile = r / size;
+}
+
+// Inclusive sum of v over lanes 0 .. lane (all 64 lanes take part).
+__device__ __forceinline__ int lane_scan_incl(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int u = __shfl_up(v, d, kWave);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
+
+// Tile map that gives each of the 8 XCDs one eighth of every expert's tiles.
+// Each expert's n_e = nt * (row tiles) tiles are taken in the order of
+// grouped_tile (L2 groups of at most gm row tiles sweeping the nt column
+// tiles); XCD x owns the contiguous slice [x n_e / 8, (x + 1) n_e / 8) of each
+// expert, and its l-th tile is found by walking its slices in expert order.
+// Against contiguous eighths of the whole tile order (xcd_tile), where one
+// XCD could hold nothing but a hot expert's full tiles while another held the
+// short tiles of small experts, every XCD now gets the same mix; a hot
+// expert's L2 groups still stay whole on one XCD.  Wave-level; false past
+// the XCD's last tile.
+__device__ __forceinline__ bool xcd_expert_tile(const ExpertRows& X, int x, int l, int bm, int nt, int gm, int& mt,
+                                                int& ntile) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int rt = (X.cnt + bm - 1) / bm;  // lane e < 32: row tiles of expert e (0 elsewhere)
+  const int n = rt * nt;                  // its tiles
+  const int lo = (int)(((int64_t)x * n) / 8), hi = (int)(((int64_t)(x + 1) * n) / 8);
+  const int size = hi - lo;               // its slice on XCD x
+  const int incl = lane_scan_incl(size);
+  if (l >= __builtin_amdgcn_readlane(incl, kWave - 1)) return false;
+  const int e = __builtin_ctzll(__ballot(incl > l));
+  const int i = __builtin_amdgcn_readlane(lo, e) + l - (__builtin_amdgcn_readlane(incl, e) - __builtin_amdgcn_readlane(size, e));
+  const int rte = __builtin_amdgcn_readlane(rt, e);
+  const int tb = __builtin_amdgcn_readlane(lane_scan_incl(rt) - rt, e);  // row tiles before expert e
+  // expert-local index i -> (row tile, column tile) in grouped_tile's order
+  const int ng = (rte + gm - 1) / gm;
+  const int j = min(i / (gm * nt), ng - 1);
+  const int o = i - j * gm * nt;
+  const int rows_g = min(gm, rte - j * gm);
+  mt = tb + j * gm + o % rows_g;
+  ntile = o / rows_g;
+  return true;
 }
 
 }  // namespace moe
