@@ -320,7 +320,8 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
 //   * workgroup = WM x WN waves, wave tile (16*MI) rows x (16*NJ) columns;
 //   * a pipeline stage is 64 K values: the bf16 activation rows (A) and the
 //     e4m3 W2 rows (B), copied global -> LDS by global_load_lds_dwordx4,
-//     4 LDS buffers (loads for stage s+3 in flight while stage s multiplies);
+//     a ring of STAGES LDS buffers (shipped: two, the copy of stage s+1 in
+//     flight while stage s multiplies);
 //   * operand fragments sit in LDS row-major with swizzled chunks: an A
 //     fragment (16 rows x 64 K bf16 = 128 B per row) is two wide planes, a B
 //     fragment (16 rows x 64 K e4m3) one narrow plane; MFMA lane L = 16*q + r
