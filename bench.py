@@ -44,6 +44,7 @@ G1_BYTES_PER_EXPERT = 2 * I * H + 32 * 56 * 4   # 29,367,296
 G2_BYTES_PER_EXPERT = H * I + 56 * 16 * 4       # 14,683,648
 HBM_PEAK = 8.0e12                  # B/s, MI355X HBM3E
 PEAK = {"fp8": 5.0e15, "bf16": 2.5e15}  # dense MFMA FLOP/s
+PEAK_CLOCK_GHZ = 2.4                # MI355X peak engine clock the MFMA peaks are quoted at
 STAGE_MFMA_DTYPE = {"gemm1_swiglu": "fp8", "gemm2": "bf16"}
 GPU_WORKLOADS = ("decode_t1", "decode_t1_s3", "small_t64", "prefill_t1024", "skewed_t8192")
 DEFAULT_WORKLOAD = "skewed_t8192"
@@ -279,13 +280,20 @@ _STAGE_OF = (("route", "route"), ("perm", "route"), ("gemm1", "gemm1_swiglu"), (
              ("combine", "combine"))
 
 
+CLOCK_MIN_US = 100.0  # shortest dispatch whose GUI_ACTIVE / duration is taken as its clock
+
+
 def live_traffic(workload, timeout_s=180):
     """HBM bytes per launch of every stage of `workload`, measured in this
     bench run: two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE; one
     counter group each) over child runs of this script (--calls-only plus a
     1 GiB device copy), each scaled so that the copy reads and writes exactly
-    1 GiB.  Called before this process touches the GPU.  Returns
-    ({stage: bytes}, None) or (None, reason)."""
+    1 GiB.  The FETCH_SIZE pass also collects GRBM_GUI_ACTIVE, which arrives
+    summed over the 8 XCDs: / 8 / the dispatch's duration is the shader clock
+    the stage's kernels ran at (stages whose dispatches last CLOCK_MIN_US or
+    more; a short dispatch's counter window is longer than the dispatch).
+    Called before this process touches the GPU.  Returns
+    ({stage: bytes}, {stage: GHz}, None) or (None, None, reason)."""
     import csv
     import glob
     import re
@@ -294,27 +302,37 @@ def live_traffic(workload, timeout_s=180):
     import tempfile
 
     if shutil.which("rocprofv3") is None:
-        return None, "rocprofv3 not found"
+        return None, None, "rocprofv3 not found"
     tmp = tempfile.mkdtemp(prefix="moe_bench_pmc_")
     env = dict(os.environ, TMPDIR="/tmp")
-    per_stage = {}
+    per_stage, clocks = {}, {}
     try:
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
             out = os.path.join(tmp, counter)
-            cmd = ["timeout", "-s", "KILL", str(timeout_s), "rocprofv3", "--pmc", counter, "--output-format", "csv",
+            pmc = [counter, "GRBM_GUI_ACTIVE"] if counter == "FETCH_SIZE" else [counter]
+            cmd = ["timeout", "-s", "KILL", str(timeout_s), "rocprofv3", "--pmc", *pmc, "--output-format", "csv",
                    "-d", out, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__), "--no-cpu", "--no-quant",
                    "--no-peaks", "--no-traffic", "--sweep", "", "--workload", workload, "--calls-only", "--steps", "3",
                    "--warmup", "1", "--copy-calib-mib", "1024"]
-            log(f"[bench] traffic: rocprofv3 --pmc {counter} pass on {workload}")
+            log(f"[bench] traffic: rocprofv3 --pmc {' '.join(pmc)} pass on {workload}")
             r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
             files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
             if not files:
-                return None, f"rocprofv3 --pmc {counter} wrote no counters (exit {r.returncode})"
-            sums, calib, calib_id = {}, None, -1
+                return None, None, f"rocprofv3 --pmc {counter} wrote no counters (exit {r.returncode})"
+            sums, calib, calib_id, gui = {}, None, -1, {}
             for f in files:
                 for row in csv.DictReader(open(f)):
                     name = row["Kernel_Name"]
                     val = float(row["Counter_Value"])
+                    if row["Counter_Name"] == "GRBM_GUI_ACTIVE":
+                        short = re.sub(r"^void ", "", name.replace("moe::(anonymous namespace)::", ""))
+                        dur_ns = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+                        for prefix, stage in _STAGE_OF:
+                            if short.startswith(prefix) and dur_ns > 0:
+                                gui.setdefault(stage, []).append((dur_ns, val / 8 / dur_ns))
+                        continue
+                    if row["Counter_Name"] != counter:
+                        continue
                     if "copyBuffer" in name:  # the last one is the 1 GiB calibration copy
                         did = int(row["Dispatch_Id"])
                         if did > calib_id:
@@ -326,11 +344,14 @@ def live_traffic(workload, timeout_s=180):
                             key = (stage, short.split("(")[0])
                             sums.setdefault(key, []).append(val)
             if not calib:
-                return None, f"no calibration copy in the {counter} pass"
+                return None, None, f"no calibration copy in the {counter} pass"
+            for stage, v in gui.items():
+                if sum(d for d, _ in v) / len(v) >= CLOCK_MIN_US * 1e3:
+                    clocks[stage] = round(sum(c for _, c in v) / len(v), 3)
             scale = 1024.0 * (1048576.0 / calib)  # KiB -> bytes, then the copy's 1 GiB
             for (stage, _), vals in sums.items():  # mean per dispatch, summed over a stage's kernels
                 per_stage[stage] = per_stage.get(stage, 0.0) + scale * sum(vals) / len(vals)
-        return {k: int(v) for k, v in per_stage.items()}, None
+        return {k: int(v) for k, v in per_stage.items()}, clocks, None
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
 
@@ -606,7 +627,8 @@ def main():
 
     # HBM traffic and kernel times first, from child processes, before this
     # process touches the GPU
-    live, live_err = (None, "--no-traffic") if (args.no_traffic or args.calls_only) else live_traffic(args.workload)
+    live, clocks, live_err = ((None, None, "--no-traffic") if (args.no_traffic or args.calls_only)
+                              else live_traffic(args.workload))
     if live_err and not args.calls_only:
         log(f"[bench] traffic: live measurement unavailable ({live_err}); using the committed summaries")
     sweep = [s for s in args.sweep.split(",") if s]
@@ -700,6 +722,18 @@ def main():
         # `frac` is against the bf16 peak of the instruction GEMM2 runs on;
         # against the dense fp8 peak the layer's target is stated in:
         roof["frac_fp8_peak"] = round(dom["frac_fp8_peak"], 4)
+    if clocks and dom["kernel"] in clocks:
+        # The published peaks assume the 2.4 GHz peak engine clock; the
+        # dominant kernel's own clock (GRBM_GUI_ACTIVE per XCD over its
+        # duration, in the FETCH_SIZE pass) scales the peak it can reach.
+        ghz = clocks[dom["kernel"]]
+        roof["clock_GHz"] = ghz
+        roof["clock_source"] = ("GRBM_GUI_ACTIVE / 8 / dispatch duration, rocprofv3 --pmc FETCH_SIZE GRBM_GUI_ACTIVE "
+                                "pass of this run (kernels serialised under counter collection)")
+        if dom["unit"] == "TFLOP/s":
+            roof["peak_at_clock"] = round(dom["peak"] * ghz / PEAK_CLOCK_GHZ, 1)
+            roof["frac_at_clock"] = round(dom["achieved"] / roof["peak_at_clock"], 4)
+        roof["clock_by_stage"] = clocks
     if peaks:
         key = {"GB/s": "hbm_read_GBps", "TFLOP/s": "mfma_bf16_TFLOPs" if dom["kernel"] == "gemm2" else "mfma_fp8_TFLOPs"}
         roof["peak_measured"] = peaks[key[dom["unit"]]]
