@@ -283,6 +283,58 @@ _STAGE_OF = (("route", "route"), ("perm", "route"), ("gemm1", "gemm1_swiglu"), (
 CLOCK_MIN_US = 100.0  # shortest dispatch whose GUI_ACTIVE / duration is taken as its clock
 
 
+def _short_kernel(name):
+    import re
+
+    return re.sub(r"^void ", "", name.replace("moe::(anonymous namespace)::", ""))
+
+
+def parse_pmc(files, counter):
+    """One --pmc pass of a --calls-only child (the CSV files it wrote) ->
+    ({stage: mean bytes per launch}, {stage: GHz}) or None without the
+    calibration copy.  `counter` (FETCH_SIZE or WRITE_SIZE, in KiB per
+    dispatch) is scaled so that the pass's last device copy (the 1 GiB
+    calibration) moves exactly 1 GiB; a stage's bytes are the mean per
+    dispatch of each of its kernels, summed.  GRBM_GUI_ACTIVE rows (summed over
+    the 8 XCDs) give each stage's clock, GUI / 8 / duration, for stages whose
+    dispatches last CLOCK_MIN_US on average."""
+    import csv
+
+    sums, calib, calib_id, gui = {}, None, -1, {}
+    for f in files:
+        for row in csv.DictReader(open(f)):
+            name = row["Kernel_Name"]
+            val = float(row["Counter_Value"])
+            if row["Counter_Name"] == "GRBM_GUI_ACTIVE":
+                short = _short_kernel(name)
+                dur_ns = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+                for prefix, stage in _STAGE_OF:
+                    if short.startswith(prefix) and dur_ns > 0:
+                        gui.setdefault(stage, []).append((dur_ns, val / 8 / dur_ns))
+                continue
+            if row["Counter_Name"] != counter:
+                continue
+            if "copyBuffer" in name:  # the last one is the 1 GiB calibration copy
+                did = int(row["Dispatch_Id"])
+                if did > calib_id:
+                    calib_id, calib = did, val
+                continue
+            short = _short_kernel(name)
+            for prefix, stage in _STAGE_OF:
+                if short.startswith(prefix):
+                    key = (stage, short.split("(")[0])
+                    sums.setdefault(key, []).append(val)
+    if not calib:
+        return None
+    scale = 1024.0 * (1048576.0 / calib)  # KiB -> bytes, then the copy's 1 GiB
+    per_stage = {}
+    for (stage, _), vals in sums.items():  # mean per dispatch, summed over a stage's kernels
+        per_stage[stage] = per_stage.get(stage, 0.0) + scale * sum(vals) / len(vals)
+    clocks = {stage: round(sum(c for _, c in v) / len(v), 3) for stage, v in gui.items()
+              if sum(d for d, _ in v) / len(v) >= CLOCK_MIN_US * 1e3}
+    return per_stage, clocks
+
+
 def live_traffic(workload, timeout_s=180):
     """HBM bytes per launch of every stage of `workload`, measured in this
     bench run: two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE; one
@@ -294,9 +346,7 @@ def live_traffic(workload, timeout_s=180):
     more; a short dispatch's counter window is longer than the dispatch).
     Called before this process touches the GPU.  Returns
     ({stage: bytes}, {stage: GHz}, None) or (None, None, reason)."""
-    import csv
     import glob
-    import re
     import shutil
     import subprocess
     import tempfile
@@ -319,44 +369,56 @@ def live_traffic(workload, timeout_s=180):
             files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
             if not files:
                 return None, None, f"rocprofv3 --pmc {counter} wrote no counters (exit {r.returncode})"
-            sums, calib, calib_id, gui = {}, None, -1, {}
-            for f in files:
-                for row in csv.DictReader(open(f)):
-                    name = row["Kernel_Name"]
-                    val = float(row["Counter_Value"])
-                    if row["Counter_Name"] == "GRBM_GUI_ACTIVE":
-                        short = re.sub(r"^void ", "", name.replace("moe::(anonymous namespace)::", ""))
-                        dur_ns = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
-                        for prefix, stage in _STAGE_OF:
-                            if short.startswith(prefix) and dur_ns > 0:
-                                gui.setdefault(stage, []).append((dur_ns, val / 8 / dur_ns))
-                        continue
-                    if row["Counter_Name"] != counter:
-                        continue
-                    if "copyBuffer" in name:  # the last one is the 1 GiB calibration copy
-                        did = int(row["Dispatch_Id"])
-                        if did > calib_id:
-                            calib_id, calib = did, val
-                        continue
-                    short = re.sub(r"^void ", "", name.replace("moe::(anonymous namespace)::", ""))
-                    for prefix, stage in _STAGE_OF:
-                        if short.startswith(prefix):
-                            key = (stage, short.split("(")[0])
-                            sums.setdefault(key, []).append(val)
-            if not calib:
+            parsed = parse_pmc(files, counter)
+            if parsed is None:
                 return None, None, f"no calibration copy in the {counter} pass"
-            for stage, v in gui.items():
-                if sum(d for d, _ in v) / len(v) >= CLOCK_MIN_US * 1e3:
-                    clocks[stage] = round(sum(c for _, c in v) / len(v), 3)
-            scale = 1024.0 * (1048576.0 / calib)  # KiB -> bytes, then the copy's 1 GiB
-            for (stage, _), vals in sums.items():  # mean per dispatch, summed over a stage's kernels
-                per_stage[stage] = per_stage.get(stage, 0.0) + scale * sum(vals) / len(vals)
+            for stage, b in parsed[0].items():
+                per_stage[stage] = per_stage.get(stage, 0.0) + b
+            clocks.update(parsed[1])
         return {k: int(v) for k, v in per_stage.items()}, clocks, None
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
 
 
 TRACE_CALLS = 20  # calls per workload in the kernel-trace child run
+
+
+def split_trace(rows, workloads, calls):
+    """Kernel-trace rows (dispatch id, kernel name, ns) of a --trace-calls
+    child -> ({workload: {"calls", "stage_us", "kernel_us"}}, None), or (None,
+    reason) when the trace does not hold one marked span per workload.  The
+    i-th trace_mark_begin .. trace_mark_end span holds the `calls` calls of
+    the i-th workload; the layer's kernels inside it are summed per stage (us
+    per call) and averaged per kernel."""
+    order = list(workloads)
+    cur, k = None, 0
+    per = {}
+    for _, name, ns in sorted(rows):
+        if "trace_mark_begin" in name:
+            cur = order[k] if k < len(order) else None
+            k += 1
+            continue
+        if "trace_mark_end" in name:
+            cur = None
+            continue
+        if cur is None:
+            continue
+        short = _short_kernel(name).split("(")[0]
+        for prefix, stage in _STAGE_OF:
+            if short.startswith(prefix):
+                d = per.setdefault(cur, {"kernels": {}, "stages": {}})
+                n, tot = d["kernels"].get(short, (0, 0))
+                d["kernels"][short] = (n + 1, tot + ns)
+                d["stages"][stage] = d["stages"].get(stage, 0) + ns
+                break
+    if k != len(order):
+        return None, f"kernel trace holds {k} workload spans, expected {len(order)}"
+    out = {}
+    for wname, d in per.items():
+        out[wname] = {"calls": calls,
+                      "stage_us": {st: round(ns / calls / 1e3, 3) for st, ns in d["stages"].items()},
+                      "kernel_us": {kn: round(tot / n / 1e3, 3) for kn, (n, tot) in d["kernels"].items()}}
+    return out, None
 
 
 def live_kernel_times(workloads, timeout_s=300):
@@ -369,7 +431,6 @@ def live_kernel_times(workloads, timeout_s=300):
     "calls": n}}, None) or (None, reason)."""
     import csv
     import glob
-    import re
     import shutil
     import subprocess
     import tempfile
@@ -392,36 +453,7 @@ def live_kernel_times(workloads, timeout_s=300):
             for row in csv.DictReader(open(f)):
                 rows.append((int(row["Dispatch_Id"]), row["Kernel_Name"], int(row["End_Timestamp"]) -
                              int(row["Start_Timestamp"])))
-        rows.sort()
-        order = list(workloads)
-        cur, k = None, 0
-        per = {}
-        for _, name, ns in rows:
-            if "trace_mark_begin" in name:
-                cur = order[k] if k < len(order) else None
-                k += 1
-                continue
-            if "trace_mark_end" in name:
-                cur = None
-                continue
-            if cur is None:
-                continue
-            short = re.sub(r"^void ", "", name.replace("moe::(anonymous namespace)::", "")).split("(")[0]
-            for prefix, stage in _STAGE_OF:
-                if short.startswith(prefix):
-                    d = per.setdefault(cur, {"kernels": {}, "stages": {}})
-                    n, tot = d["kernels"].get(short, (0, 0))
-                    d["kernels"][short] = (n + 1, tot + ns)
-                    d["stages"][stage] = d["stages"].get(stage, 0) + ns
-                    break
-        if k != len(order):
-            return None, f"kernel trace holds {k} workload spans, expected {len(order)}"
-        out = {}
-        for wname, d in per.items():
-            out[wname] = {"calls": TRACE_CALLS,
-                          "stage_us": {st: round(ns / TRACE_CALLS / 1e3, 3) for st, ns in d["stages"].items()},
-                          "kernel_us": {kn: round(tot / n / 1e3, 3) for kn, (n, tot) in d["kernels"].items()}}
-        return out, None
+        return split_trace(rows, workloads, TRACE_CALLS)
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
 
