@@ -67,6 +67,14 @@ LAYER_CASES = [
     ("skewed_t8192", None, 4096, None),
     # the contest dataset's largest T (moe.py:13), every token
     ("skewed_t8192", None, 14107, None),
+    # odd token counts on every kernel path, each with another routing window
+    ("prefill_t1024", 96, 3, None),
+    ("prefill_t1024", 160, 13, None),
+    ("prefill_t1024", 64, 47, None),
+    ("prefill_t1024", 192, 333, None),
+    ("prefill_t1024", 128, 777, None),
+    ("prefill_t1024", 32, 1537, None),
+    ("prefill_t1024", 224, 3001, None),
 ]
 
 
