@@ -747,7 +747,7 @@ def main():
             "kernel_us_source": dom["ms_source"], "kernel_us_events": round(dom["event_ms"] * 1e3, 3)}
     if live:
         roof["traffic_by_stage"] = live
-    if dom["kernel"] == "gemm2":
+    if dom["kernel"] == "gemm2" and dom["algo_flops"]:  # (a workload without expert work has none)
         # the activation enters as a bf16 (hi, lo) pair: two bf16 MFMAs per product
         roof["mfma_flops_executed"] = 2 * dom["algo_flops"]
         roof["executed_frac"] = round(2 * dom["frac"], 4)
