@@ -669,8 +669,10 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
   ExpertRows X;
   X.load(expert_off);
   // An eighth of every expert's tiles per XCD (xcd_expert_tile): block b
-  // takes tiles b / 8, b / 8 + cap, ... of XCD b % 8 (one: an XCD holds at most
-  // 32 tiles more than an eighth of all, within the grid's margin).
+  // takes tiles b / 8, b / 8 + cap, ... of XCD b % 8, cap being the blocks per
+  // XCD.  The grid has a block per possible tile, so a block nearly always
+  // takes one tile; the loop covers an XCD that holds more than cap (an XCD
+  // holds up to 32 tiles more than an eighth of all).
   const int xcd = blockIdx.x % 8, cap = gridDim.x / 8;
 #pragma unroll 1
   for (int li = blockIdx.x / 8;; li += cap) {
