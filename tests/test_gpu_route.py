@@ -50,17 +50,39 @@ def test_route_matches_oracle(pkg, orc, cuda_device, name, offset, T):
     cfg = pkg.synth.CONFIGS[name]
     off = cfg.local_expert_offset if offset is None else offset
     tok, host = gpu_tokens(pkg, cfg, cuda_device, T)
+    print(f"route case {name} offset={off} T={tok[0].shape[0]}", flush=True)
+    check_route(pkg, orc, tok, host, off, cfg.routed_scaling_factor)
+
+
+# More logits and biases: the generator's seeds 10-25 (none is a config's own),
+# each with another local window, so that many more score patterns meet the
+# ranking, the near-tie rule and the permutation.
+SEED_SWEEP = [(s, 32 * (s % 8)) for s in range(10, 26)]
+
+
+@pytest.mark.parametrize("seed,offset", SEED_SWEEP)
+def test_route_seed_sweep(pkg, orc, cuda_device, seed, offset):
+    cfg = pkg.synth.CONFIGS["prefill_t1024"]
+    tok = pkg.synth.tokens(cfg, cuda_device, 512, seed=seed)
+    host = (tok[0].cpu().numpy(), tok[1].view(torch.int16).cpu().numpy().view(np.uint16))
+    print(f"route seed sweep seed={seed} offset={offset} T=512", flush=True)
+    check_route(pkg, orc, tok, host, offset, cfg.routed_scaling_factor)
+
+
+def check_route(pkg, orc, tok, host, off, rsf):
+    """Expert ids equal the oracle's (moe.py:123-158) outside near-ties of the
+    fp32 scores, weights bit-exact where the ids agree, and the permutation is
+    the oracle's (ascending token order per expert, moe.py:174-178)."""
     T = tok[0].shape[0]
-    print(f"route case {name} offset={off} T={T}", flush=True)
-    r = pkg.route(tok[0], tok[1], off, cfg.routed_scaling_factor)
+    r = pkg.route(tok[0], tok[1], off, rsf)
     torch.cuda.synchronize()
     ids = r.topk_ids.cpu().numpy()
     w = r.topk_w.cpu().numpy()
-    ref_ids, ref_w = orc.route(host[0], host[1], cfg.routed_scaling_factor)
+    ref_ids, ref_w = orc.route(host[0], host[1], rsf)
 
     # ids ascending per token, 8 distinct
     assert (np.diff(ids, axis=1) > 0).all()
-    tie = near_tie_tokens(host[0], host[1], cfg.routed_scaling_factor)
+    tie = near_tie_tokens(host[0], host[1], rsf)
     same = (ids == ref_ids).all(axis=1)
     mismatch = np.nonzero(~same & ~tie)[0]
     assert mismatch.size == 0, f"expert ids differ at tokens {mismatch[:8]}"
