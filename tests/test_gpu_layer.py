@@ -80,15 +80,35 @@ LAYER_CASES = [
 
 @pytest.mark.parametrize("name,offset,T,n_check", LAYER_CASES)
 def test_layer_matches_oracle(pkg, orc, cuda_device, name, offset, T, n_check):
-    """Every checked token whose routed expert ids equal the oracle's is
-    compared element-wise; a token whose ids differ must be a near-tie of the
-    fp32 scores (and is then left out)."""
     cfg = pkg.synth.CONFIGS[name]
     off = cfg.local_expert_offset if offset is None else offset
     w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
     tok, host = gpu_tokens(pkg, cfg, cuda_device, T)
+    print(f"layer case {name} offset={off} T={tok[0].shape[0]}", flush=True)
+    check_layer(pkg, orc, cuda_device, cfg, off, tok, host, w, w_host, n_check)
+
+
+# Other weights and tokens: generator seeds no config uses, each with another
+# local window and a T on another kernel path (streaming, tiled, wide GEMM1).
+SEED_CASES = [(5, 64, 50), (7, 160, 600), (9, 224, 1500)]
+
+
+@pytest.mark.parametrize("seed,offset,T", SEED_CASES)
+def test_layer_seed_sweep(pkg, orc, cuda_device, seed, offset, T):
+    cfg = pkg.synth.CONFIGS["prefill_t1024"]
+    w, w_host = gpu_weights(pkg, seed, cuda_device)
+    tok = pkg.synth.tokens(cfg, cuda_device, T, seed=seed)
+    host = (tok[0].cpu().numpy(), tok[1].view(torch.int16).cpu().numpy().view(np.uint16),
+            tok[2].view(torch.uint8).cpu().numpy(), tok[3].cpu().numpy())
+    print(f"layer seed case seed={seed} offset={offset} T={T}", flush=True)
+    check_layer(pkg, orc, cuda_device, cfg, offset, tok, host, w, w_host, None)
+
+
+def check_layer(pkg, orc, cuda_device, cfg, off, tok, host, w, w_host, n_check):
+    """Every checked token whose routed expert ids equal the oracle's is
+    compared element-wise; a token whose ids differ must be a near-tie of the
+    fp32 scores (and is then left out)."""
     T = tok[0].shape[0]
-    print(f"layer case {name} offset={off} T={T}", flush=True)
     out = run_layer(pkg, tok, w, off, cfg.routed_scaling_factor).float().cpu().numpy()
     assert np.isfinite(out).all(), "output not fully written / non-finite"
     gpu_ids = pkg.intermediates(pkg.workspace(cuda_device, T), T).topk_ids.cpu().numpy()
