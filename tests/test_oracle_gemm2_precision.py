@@ -14,7 +14,9 @@ Pinned here (the layer already puts 33 / 680 elements outside at x30 / x300
 through GEMM1's fp8 block sums, GPU test_gpu_precision.py):
   * the shipped pair adds almost nothing;
   * three e4m3 terms (3/4 of the pair's MFMA time) add several hundred at x300;
-  * bf16 hi + e4m3 lo fails hundreds already at x30.
+  * bf16 hi + e4m3 lo fails hundreds already at x30;
+  * one fp16 term with a power-of-two scale per (row, 128 columns), which
+    would halve GEMM2's MFMA work, fails thousands at x30.
 """
 import numpy as np
 import pytest
@@ -47,6 +49,18 @@ def _block_e4m3(x):
     return (_e4m3(xb / s) * s).reshape(n, -1)
 
 
+def _fp16_scaled(v):
+    """One fp16 term (11 significant bits, f16 MFMA at the bf16 rate) with a
+    power-of-two scale per (row, 128 columns) that puts the block's largest
+    magnitude in [2^14, 2^15), inside fp16's range."""
+    n = v.shape[0]
+    vb = v.reshape(n, -1, 128)
+    m = np.abs(vb).max(axis=2, keepdims=True)
+    e = np.floor(np.log2(np.where(m > 0, m, 1.0)))
+    s = np.ldexp(1.0, (e - 14).astype(np.int64))
+    return ((vb / s).astype(np.float16).astype(np.float64) * s).reshape(n, -1)
+
+
 def _representations(c):
     v = c.astype(np.float64)
     hi = _bf16(c)
@@ -58,6 +72,7 @@ def _representations(c):
         "bf16_pair": hi.astype(np.float64) + lo.astype(np.float64),
         "e4m3_x3": t1 + t2 + t3,
         "bf16hi_e4m3lo": hi.astype(np.float64) + _block_e4m3(v - hi.astype(np.float64)),
+        "fp16_scaled": _fp16_scaled(v),
     }
 
 
@@ -108,3 +123,5 @@ def test_gemm2_activation_representations(case):
     assert f300["e4m3_x3"] >= 3 * max(f300["bf16_pair"], 1)
     assert f300["e4m3_x3"] >= 200
     assert f30["bf16hi_e4m3lo"] >= 100
+    # one scaled fp16 term (half the pair's MFMA work): thousands at x30
+    assert f30["fp16_scaled"] >= 1000
