@@ -16,7 +16,9 @@ through GEMM1's fp8 block sums, GPU test_gpu_precision.py):
   * three e4m3 terms (3/4 of the pair's MFMA time) add several hundred at x300;
   * bf16 hi + e4m3 lo fails hundreds already at x30;
   * one fp16 term with a power-of-two scale per (row, 128 columns), which
-    would halve GEMM2's MFMA work, fails thousands at x30.
+    would halve GEMM2's MFMA work, fails thousands at x30;
+  * that fp16 term plus an e4m3 remainder stays clean at x30 and adds a few
+    dozen at x300 over the pair.
 """
 import numpy as np
 import pytest
@@ -73,6 +75,7 @@ def _representations(c):
         "e4m3_x3": t1 + t2 + t3,
         "bf16hi_e4m3lo": hi.astype(np.float64) + _block_e4m3(v - hi.astype(np.float64)),
         "fp16_scaled": _fp16_scaled(v),
+        "fp16hi_e4m3lo": _fp16_scaled(v) + _block_e4m3(v - _fp16_scaled(v)),
     }
 
 
@@ -125,3 +128,6 @@ def test_gemm2_activation_representations(case):
     assert f30["bf16hi_e4m3lo"] >= 100
     # one scaled fp16 term (half the pair's MFMA work): thousands at x30
     assert f30["fp16_scaled"] >= 1000
+    # scaled fp16 hi + e4m3 lo (3/4 of the pair's work, the lo term on the fp8
+    # MFMA's K = 128): as good as the pair at x30, somewhat worse at x300
+    assert f30["fp16hi_e4m3lo"] == 0 and f300["bf16_pair"] < f300["fp16hi_e4m3lo"] <= 200
