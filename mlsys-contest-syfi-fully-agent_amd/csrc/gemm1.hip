@@ -387,8 +387,10 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
 // Both kernels give the same output bits.
 constexpr int kGemm1TiledLargeMinTokens = 1025;
 
-template <int WM, int WN, int MI>
+template <int WM, int WN, int MI, int ST>
 struct G1Tiled {
+  static constexpr int kWN = WN;
+  static constexpr int kMI = MI;
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = kWave * kWaves;
   static constexpr int BM = 16 * MI * WM;       // rows per tile
@@ -405,55 +407,96 @@ struct G1Tiled {
   // kScaleRowsPerWave entries are its rows' scales.
   static constexpr int kStageBytes = kSOff + kWaves * kWave * 4;
   static constexpr int kWscBytes = WN * 2 * kNHBlk * 4;  // weight block scales (after the stages)
-  static constexpr int kStages = 3;
+  static constexpr int kStages = ST;
   static_assert(kStages >= 2 && kStages <= 6, "pipeline depth (wait_stages_ahead)");
+  static constexpr int kRingBytes = kStages * kStageBytes;
   static constexpr int kPlanes = 2 * (kAFrags + kBFrags);
   static_assert(kPlanes % kWaves == 0, "planes must split evenly over waves");
   static constexpr int kPlanesPerWave = kPlanes / kWaves;
   static constexpr int kScaleRowsPerWave = BM / kWaves;
   static_assert(kScaleRowsPerWave % 4 == 0 && kScaleRowsPerWave <= kWave, "scale rows per wave");
   static constexpr int kDmaPerStage = kPlanesPerWave + 1;
-  static constexpr int kGroupM = 4;             // at most this many row tiles (of one expert) per L2 group
 };
 
-template <int WM, int WN, int MI>
-__global__ void __launch_bounds__(64 * WM * WN, 4)
-gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
-                   const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
-                   const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
-                   uint16_t* __restrict__ act) {
-  using C = G1Tiled<WM, WN, MI>;
-  // One LDS object: the stage ring, then the weight scale table.  (A second
-  // __shared__ array makes the compiler wait for every outstanding LDS DMA
-  // before any LDS read, which would serialise the pipeline.)
-  __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
+// Two tile heights.  Short tiles hold up to 64 rows of one expert (one 16-row
+// block per wave, a 3-stage ring); tall tiles 65-128 rows (two blocks per
+// wave, a 2-stage ring), so the W13 columns of those rows pass through the
+// copy path once instead of once per 64 rows -- the copy path (about 9.5 TB/s
+// of L2 -> LDS over the chip), not HBM, bounds this kernel.  Rows past a
+// tile's last row copy its last row again, which costs the copy path nothing
+// (lanes given an out-of-range buffer offset instead changed no time).  Both
+// rings fit one LDS array of the short ring's size: two workgroups per CU.
+// A tall tile costs about 1.5 short ones; with few tiles per workgroup one
+// tall tile can outlast two short ones, so each launch chooses between tall
+// tiles and short tiles only from the row counts (G1TiledPaths::use_tall).
+template <int WM, int WN>
+struct G1TiledPaths {
+  using Short = G1Tiled<WM, WN, 1, 3>;
+  using Tall = G1Tiled<WM, WN, 2, 2>;
+  static_assert(2 * Short::BM == Tall::BM && Short::kNT == Tall::kNT, "a tall tile is two short ones");
+  static constexpr int BM = Tall::BM;           // tile height of the tile map
+  static constexpr int kNT = Short::kNT;
+  static constexpr int kThreads = Short::kThreads;
+  static constexpr int kGroupM = 4;             // at most this many row tiles (of one expert) per L2 group
+  static constexpr int kRingBytes = Short::kRingBytes > Tall::kRingBytes ? Short::kRingBytes : Tall::kRingBytes;
+  static constexpr int kLdsBytes = kRingBytes + Short::kWscBytes;
+  // Tall tiles (and the tall-first map) or short tiles only, for a grid of
+  // `slots` resident workgroups.  In short-tile units a tall tile costs 1.5,
+  // so the work is W = 1.5 tall + short against S short tiles.  Tall tiles
+  // pay (a) when they fit the work into one round of slots that the short
+  // tiles overflow, or (b) when the short tiles take at least 1.6 rounds and W
+  // saves 5 %.  Below one round the short map runs an expert's two short
+  // tiles side by side, faster than one tall tile; between one and 1.6 rounds
+  // both maps end in a partial round, and tall tiles lengthen the first.
+  // Interleaved A/B, GEMM1 us (short tiles only -> this rule's choice):
+  // prefill routing T = 1024 157.7 -> 138.6, 896 154.9 -> 136.3, 768 142.6 ->
+  // 129.1, 640 137.6 -> 126.6; hot experts T = 1024 269.2 -> 214.6, 512
+  // 168.6 -> 149.3, 256 118.7 -> 104.8, 128 94.5 -> 82.7.  Tall tiles where
+  // the rule keeps the short map: prefill T = 512 106.4 -> 111.8, 384 103.5 ->
+  // 109.8; hot experts T = 192 93.8 -> 99.9, 96 65.1 -> 76.1, 65 62.1 -> 71.9.
+  __device__ static bool use_tall(const ExpertRows& X, int slots) {
+    int n_tall, n_short;
+    tall_short_row_tiles(X, BM, n_tall, n_short);
+    const int s_rows = X.count_tiles(Short::BM);  // short-map row tiles
+    const int w2 = 3 * n_tall + 2 * n_short;       // 2 W in row tiles
+    const bool one_round = s_rows * kNT > slots && w2 * kNT <= 2 * slots;
+    const bool saves = 5 * s_rows * kNT >= 8 * slots && 10 * w2 <= 19 * s_rows;
+    return n_tall > 0 && (one_round || saves);
+  }
+};
 
-  // ---- tile of this workgroup ------------------------------------------
-  ExpertRows X;
-  X.load(expert_off);
-  const int mt_total = X.count_tiles(C::BM);
-  // Persistent: the grid is at most what fits on the device at once; each
-  // workgroup walks its tiles (no workgroup is launched past the last tile).
-#pragma unroll 1
-  for (int it = 0;; ++it) {
-  const int t = xcd_tile_nth(blockIdx.x, gridDim.x, mt_total * C::kNT, it);
-  if (t < 0) break;
-  if (it > 0) block_barrier();  // every wave is done with the previous tile's LDS
-  int mt, nt;
-  grouped_tile(X, t, C::BM, C::kNT, C::kGroupM, mt, nt);
-  int e, row0, rows;
-  X.find_tile(mt, C::BM, e, row0, rows);
-  const int j0 = nt * C::kGateCols;
-
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform (SGPR)
-  const int lane = threadIdx.x & (kWave - 1);
+// One tile: `rows` rows of expert e from permuted row row0, gate columns
+// j0 .. j0 + kGateCols - 1 and the matching up columns.  `lds` is the
+// kernel's one LDS object (the stage ring), `wsc` the weight scale table
+// after it.  Every wave of the workgroup calls it; the caller's barrier
+// separates consecutive tiles.
+template <class C>
+__device__ __forceinline__ void gemm1_tile(char* lds, float* wsc, const uint8_t* __restrict__ hs,
+                                           const float* __restrict__ hs_scale, int T,
+                                           const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
+                                           const int32_t* __restrict__ perm_token, uint16_t* __restrict__ act,
+                                           int e, int row0, int rows, int j0, bool w_once) {
+  constexpr int WN = C::kWN, MI = C::kMI;
+  // The thread index is opaque to the optimiser: values derived from it are
+  // computed per tile, not hoisted out of the tile loop and kept live
+  // (spilled) across the tall path, which needs all 128 VGPRs.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform (SGPR)
+  const int lane = tid & (kWave - 1);
   const int lq = lane >> 4;
   const int lr = lane & 15;
   const int wm = wave / WN;
   const int wn = wave % WN;
 
-  // ---- per-lane DMA sources (kb = 0) -------------------------------------
-  const uint8_t* src[C::kPlanesPerWave];
+  // ---- DMA planes of this wave: planes wave + 8k; the first kAPlanes are
+  // hidden rows (A), the rest W13 rows (B).  Sources are a wave-uniform base
+  // plus a 32-bit lane offset, one VGPR per plane (T <= 1024 here, so every
+  // offset fits).
+  constexpr int kAPlanes = 2 * C::kAFrags / C::kWaves;
+  static_assert((2 * C::kAFrags) % C::kWaves == 0, "A planes split evenly over the waves");
+  const uint8_t* w13e = w13 + (size_t)e * k2I * kH;
+  uint32_t off[C::kPlanesPerWave];
   int dst[C::kPlanesPerWave];
 #pragma unroll
   for (int k = 0; k < C::kPlanesPerWave; ++k) {
@@ -461,45 +504,44 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
     const int frag = plane >> 1, half = plane & 1;
     int fr, chunk;
     wide_copy_lane(lane, half, fr, chunk);
-    if (frag < C::kAFrags) {
+    if (k < kAPlanes) {
       const int r = min(frag * 16 + fr, rows - 1);
-      src[k] = hs + (size_t)perm_token[row0 + r] * kH + 16 * chunk;
+      off[k] = (uint32_t)perm_token[row0 + r] * kH + 16 * chunk;
       dst[k] = frag * C::kFrag + half * 1024;
     } else {
       const int bf = frag - C::kAFrags;
       const int n = bf < 2 * WN ? j0 + 16 * bf + fr : kI + j0 + 16 * (bf - 2 * WN) + fr;
-      src[k] = w13 + ((size_t)e * k2I + n) * kH + 16 * chunk;
+      off[k] = (uint32_t)n * kH + 16 * chunk;
       dst[k] = C::kBOff + bf * C::kFrag + half * 1024;
     }
   }
   // lanes past the wave's rows copy the first row's scale again (one cache
   // line instead of one per lane; their slot entries are never read)
   const int srow = wave * C::kScaleRowsPerWave + (lane < C::kScaleRowsPerWave ? lane : 0);
-  const float* ssrc = hs_scale + perm_token[row0 + min(srow, rows - 1)];
+  const uint32_t stok = (uint32_t)perm_token[row0 + min(srow, rows - 1)];
   const int sdst = C::kSOff + wave * kWave * 4;
 
   // The W13 tile of an expert with a single row tile is read exactly once:
   // its copies take the nontemporal policy (T = 128: GEMM1 88.1 -> 77.5 us,
   // T = 1024 181.3 -> 174.4 us).  Experts of several row tiles re-read it
   // through L2 and keep the default (nt everywhere made T = 1024 8 % slower).
-  const bool w_once = X.end(e) - X.begin(e) <= C::BM;
   auto issue = [&](int kb) {
     char* base = lds + (kb % C::kStages) * C::kStageBytes;
 #pragma unroll
     for (int k = 0; k < C::kPlanesPerWave; ++k) {
-      const bool b_plane = ((wave + k * C::kWaves) >> 1) >= C::kAFrags;
-      if (b_plane && w_once)
-        dma16_nt(src[k] + kb * kBlk, base + dst[k]);
+      if (k < kAPlanes)
+        dma16(hs + kb * kBlk + off[k], base + dst[k]);
+      else if (w_once)
+        dma16_nt(w13e + kb * kBlk + off[k], base + dst[k]);
       else
-        dma16(src[k] + kb * kBlk, base + dst[k]);
+        dma16(w13e + kb * kBlk + off[k], base + dst[k]);
     }
-    dma4(ssrc + (size_t)kb * T, base + sdst);
+    dma4(hs_scale + (size_t)kb * T + stok, base + sdst);
   };
 
   // Weight block scales of every wave's gate / up columns, staged in LDS once
   // (no scalar loads in the main loop: they would force full lgkmcnt waits).
-  float* wsc = (float*)(lds + C::kStages * C::kStageBytes);  // [WN][2][56]
-  for (int i = threadIdx.x; i < WN * 2 * kNHBlk; i += C::kThreads) {
+  for (int i = tid; i < WN * 2 * kNHBlk; i += C::kThreads) {  // [WN][2][56]
     const int w_n = i / (2 * kNHBlk), up = (i / kNHBlk) & 1, kb = i % kNHBlk;
     const int blk = (up ? kI : 0) + j0 + 32 * w_n;
     wsc[i] = w13_scale[((size_t)e * kN2IBlk + blk / kBlk) * kNHBlk + kb];
@@ -593,21 +635,75 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
           p[64] = lo;
         }
       }
+}
+
+template <int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN, 4)
+gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
+                   const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
+                   const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
+                   uint16_t* __restrict__ act) {
+  using P = G1TiledPaths<WM, WN>;
+  // One LDS object: the stage ring, then the weight scale table.  (A second
+  // __shared__ array makes the compiler wait for every outstanding LDS DMA
+  // before any LDS read, which would serialise the pipeline.)
+  __shared__ __attribute__((aligned(1024))) char lds[P::kLdsBytes];
+  float* wsc = (float*)(lds + P::kRingBytes);  // [WN][2][56]
+
+  // Persistent: the grid is at most what fits on the device at once; each
+  // workgroup walks its tiles (no workgroup is launched past the last tile).
+  // Short map: contiguous eighths of the 64-row tile order per XCD.  Tall
+  // map: xcd_tall_first_tile, block b taking XCD b % 8's tiles b / 8 in the
+  // first round, then in reverse order (snake), so that the blocks that ran a
+  // tall tile first take a second tile last.  The expert offsets are read
+  // again for every tile (one L2 load) rather than kept in two VGPRs across
+  // the tall path, which needs all 128.
+  bool tall_map;
+  {
+    ExpertRows X;
+    X.load(expert_off);
+    tall_map = P::use_tall(X, gridDim.x);  // the same in every workgroup
+  }
+  const int xcd = blockIdx.x % 8, cap = gridDim.x / 8, slot = blockIdx.x / 8;
+#pragma unroll 1
+  for (int it = 0;; ++it) {
+    ExpertRows X;
+    X.load(expert_off);
+    int mt, nt, e, row0, rows;
+    if (tall_map) {
+      const int li = (it & 1) ? (it + 1) * cap - 1 - slot : it * cap + slot;
+      if (!xcd_tall_first_tile(X, xcd, li, P::BM, P::kNT, P::kGroupM, mt, nt)) break;
+      X.find_tile(mt, P::BM, e, row0, rows);
+    } else {
+      const int t = xcd_tile_nth(blockIdx.x, gridDim.x, X.count_tiles(P::Short::BM) * P::kNT, it);
+      if (t < 0) break;
+      grouped_tile(X, t, P::Short::BM, P::kNT, P::kGroupM, mt, nt);
+      X.find_tile(mt, P::Short::BM, e, row0, rows);
+    }
+    if (it > 0) block_barrier();  // every wave is done with the previous tile's LDS
+    const int j0 = nt * P::Short::kGateCols;
+    const bool w_once = X.end(e) - X.begin(e) <= (tall_map ? P::BM : P::Short::BM);  // one row tile
+    if (rows > P::Short::BM)  // workgroup-uniform
+      gemm1_tile<typename P::Tall>(lds, wsc, hs, hs_scale, T, w13, w13_scale, perm_token, act, e, row0, rows, j0,
+                                   w_once);
+    else
+      gemm1_tile<typename P::Short>(lds, wsc, hs, hs_scale, T, w13, w13_scale, perm_token, act, e, row0, rows, j0,
+                                    w_once);
   }
 }
 
-template <int WM, int WN, int MI>
+template <int WM, int WN>
 hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
                               const float* w13_scale, const Layout& L, char* ws, hipStream_t stream) {
-  using C = G1Tiled<WM, WN, MI>;
+  using P = G1TiledPaths<WM, WN>;
   const int64_t pairs = (int64_t)T * kTopK;
-  const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
-  static ResidentGrid resident(gemm1_tiled_kernel<WM, WN, MI>, C::kThreads);
-  const int64_t upper = ((mtiles * C::kNT + 7) / 8) * 8;
+  const int64_t mtiles = (pairs + P::Short::BM - 1) / P::Short::BM + (pairs < kELocal ? pairs : kELocal);
+  static ResidentGrid resident(gemm1_tiled_kernel<WM, WN>, P::kThreads);
+  const int64_t upper = ((mtiles * P::kNT + 7) / 8) * 8;
   const int resident_n = resident.count();
   const int64_t cap = resident_n >= 8 ? resident_n / 8 * 8 : 8;
   const int64_t blocks = upper < cap ? upper : cap;
-  hipLaunchKernelGGL((gemm1_tiled_kernel<WM, WN, MI>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
+  hipLaunchKernelGGL((gemm1_tiled_kernel<WM, WN>), dim3((unsigned)blocks), dim3(P::kThreads), 0,
                      stream, hs, hs_scale, T, w13, w13_scale, (const int32_t*)(ws + L.expert_off),
                      (const int32_t*)(ws + L.perm_token), (uint16_t*)(ws + L.act));
   return hipGetLastError();
@@ -925,7 +1021,7 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const u
     }
     return hipGetLastError();
   }
-  if (T < kGemm1TiledLargeMinTokens) return launch_gemm1_tiled<4, 2, 1>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
+  if (T < kGemm1TiledLargeMinTokens) return launch_gemm1_tiled<4, 2>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
   return launch_gemm1_wide(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
 }
 

@@ -527,4 +527,60 @@ __device__ __forceinline__ bool xcd_expert_tile(const ExpertRows& X, int x, int 
   return true;
 }
 
+
+// Row tiles of two heights: an expert's row tiles hold bm rows, its last one
+// fewer; a last row tile of at most bm / 2 rows is "short", every other row
+// tile "tall".  Totals over the experts (wave-level, uniform results).
+__device__ __forceinline__ void tall_short_row_tiles(const ExpertRows& X, int bm, int& n_tall, int& n_short) {
+  const int rt = (X.cnt + bm - 1) / bm;  // lane e < 32: row tiles of expert e
+  const int sh = rt > 0 && X.cnt - (rt - 1) * bm <= bm / 2 ? 1 : 0;
+  n_short = __builtin_amdgcn_readlane(lane_scan_incl(sh), kWave - 1);
+  n_tall = __builtin_amdgcn_readlane(lane_scan_incl(rt), kWave - 1) - n_short;
+}
+
+// Tile map for those two heights.  XCD x takes an eighth of every expert's
+// tall tiles and an eighth of its short tiles (as xcd_expert_tile does for one
+// height); its list holds all its tall tiles (expert order, grouped_tile order
+// inside an expert) before its short ones, so that the longer tiles start
+// first.  mt is the row tile in ExpertRows::find_tile(mt, bm) numbering.
+// Wave-level; false past the XCD's last tile.
+__device__ __forceinline__ bool xcd_tall_first_tile(const ExpertRows& X, int x, int l, int bm, int nt, int gm,
+                                                    int& mt, int& ntile) {
+  const int rt = (X.cnt + bm - 1) / bm;
+  const int sh = rt > 0 && X.cnt - (rt - 1) * bm <= bm / 2 ? 1 : 0;  // its last row tile is short
+  const int tall = rt - sh;
+  const int tb = lane_scan_incl(rt) - rt;  // row tiles before expert e
+  {
+    const int n = tall * nt;
+    const int lo = (int)(((int64_t)x * n) / 8), hi = (int)(((int64_t)(x + 1) * n) / 8);
+    const int size = hi - lo;
+    const int incl = lane_scan_incl(size);
+    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+    if (l < total) {
+      const int e = __builtin_ctzll(__ballot(incl > l));
+      const int i = __builtin_amdgcn_readlane(lo, e) + l -
+                    (__builtin_amdgcn_readlane(incl, e) - __builtin_amdgcn_readlane(size, e));
+      const int rte = __builtin_amdgcn_readlane(tall, e);
+      const int ng = (rte + gm - 1) / gm;
+      const int j = min(i / (gm * nt), ng - 1);
+      const int o = i - j * gm * nt;
+      const int rows_g = min(gm, rte - j * gm);
+      mt = __builtin_amdgcn_readlane(tb, e) + j * gm + o % rows_g;
+      ntile = o / rows_g;
+      return true;
+    }
+    l -= total;
+  }
+  const int n = sh * nt;
+  const int lo = (int)(((int64_t)x * n) / 8), hi = (int)(((int64_t)(x + 1) * n) / 8);
+  const int size = hi - lo;
+  const int incl = lane_scan_incl(size);
+  if (l >= __builtin_amdgcn_readlane(incl, kWave - 1)) return false;
+  const int e = __builtin_ctzll(__ballot(incl > l));
+  ntile = __builtin_amdgcn_readlane(lo, e) + l -
+          (__builtin_amdgcn_readlane(incl, e) - __builtin_amdgcn_readlane(size, e));
+  mt = __builtin_amdgcn_readlane(tb, e) + __builtin_amdgcn_readlane(tall, e);  // the expert's last row tile
+  return true;
+}
+
 }  // namespace moe
