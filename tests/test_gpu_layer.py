@@ -59,6 +59,10 @@ LAYER_CASES = [
     ("skewed_t8192", None, 64, None),
     ("skewed_t8192", None, 40, None),
     ("prefill_t1024", None, 65, None),    # first T with the tiled GEMM1 and a combine pass
+    # tiled GEMM1 tall tiles: two tall + one short tile of exactly 64 rows per
+    # hot expert; prefill routing with tall and short tiles
+    ("skewed_t8192", None, 320, None),
+    ("prefill_t1024", None, 704, None),
     ("skewed_t8192", None, 1024, None),   # largest T of the tiled GEMM1
     ("skewed_t8192", None, 1025, None),   # smallest T of the wide GEMM1
     ("skewed_t8192", None, 2047, None),
@@ -160,6 +164,13 @@ INTERMEDIATE_CASES = [
     # past a tile's rows are skipped per wave (0, 1 or 2 live blocks)
     ("prefill_t1024", 320, None),
     ("small_t64", 256, None),
+    # tiled GEMM1 tile heights (64-row short tiles, 128-row tall tiles, chosen
+    # per launch): the hot experts take every token, so T sets their rows.
+    ("skewed_t8192", 128, None),        # tall map, experts of exactly 128 rows
+    ("skewed_t8192", 129, None),        # short map, experts of 64 + 64 + 1 rows
+    ("skewed_t8192", 193, None),        # tall map, a second tall tile of 65 rows
+    ("skewed_t8192", 321, 400),         # tall map, three tall tiles, the last of 65 rows
+    ("prefill_t1024", 704, 400),        # tall map, partly filled tall tiles among short ones
 ]
 
 
