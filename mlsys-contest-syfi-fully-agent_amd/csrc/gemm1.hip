@@ -378,14 +378,28 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
 //   * per K block: P = A_f8 * B_f8 (v_mfma_f32_16x16x128_f8f6f4, exact
 //     products), acc += P * (a_scale[row] * w_scale[n/128]).
 // ---------------------------------------------------------------------------
-// Token count from which GEMM1 uses the wide 256 x 256 tiles.  Below it,
-// experts have few rows, and 64-row x 64-gate-column tiles of 8 waves give
-// more workgroups to stream the weights.  Measured: at T = 1536 the wide
-// tiles win with uniform routing (222 against 234 us) and with four hot
-// experts (319 against 430 us); at T = 1024 the tiled kernel wins with uniform
-// routing (188 against 206 us) and loses with hot experts (320 against 222 us).
-// Both kernels give the same output bits.
+// Kernel choice by T: the tiled kernel up to kGemm1TiledLargeMinTokens - 1,
+// both launched up to kGemm1BothMaxTokens (each exits unless the row counts
+// choose it, wide_tiles_full), the wide 256 x 256 tiles beyond.  Both give
+// the same output bits.  The wide tiles pay when a few experts hold most rows
+// (their 256-row tiles then mostly full); with rows spread over many experts
+// the tiled kernel's 64- and 128-row tiles copy less and fill two workgroups
+// per CU.  Interleaved A/B, GEMM1 us, wide -> tiled: prefill routing
+// T = 1025 184.0 -> 139.5, 1280 188.9 -> 146.6, 1536 179.4 -> 167.3, 2048
+// 198.8 -> 198.1; small_t64 routing T = 1100 182.8 -> 147.0, 1536 188.3 ->
+// 166.8, 2048 193.5 -> 191.5; four hot experts T = 1025 196.7 -> 216.6, 1536
+// 268.1 -> 297.2, 2048 317.7 -> 369.0 (wide tile fill 0.20-0.39 without hot
+// experts, 0.54-0.74 with them).  Past T = 1536 the spread case is a tie,
+// and launching both would cost the exiting kernel's ~3 us.
 constexpr int kGemm1TiledLargeMinTokens = 1025;
+constexpr int kGemm1BothMaxTokens = 1536;
+
+// True when the wide kernel's 256-row tiles would be at least 45 % full.
+// Wave-level; the same in every workgroup of both kernels.
+__device__ __forceinline__ bool wide_tiles_full(const ExpertRows& X) {
+  const int rows = __builtin_amdgcn_readlane(lane_scan_incl(X.cnt), kWave - 1);
+  return 100 * rows >= 45 * 256 * X.count_tiles(256);
+}
 
 template <int WM, int WN, int MI, int ST>
 struct G1Tiled {
@@ -637,12 +651,14 @@ __device__ __forceinline__ void gemm1_tile(char* lds, float* wsc, const uint8_t*
       }
 }
 
+// both: launched together with the wide kernel; runs only if the row counts
+// choose the tiled tiles (!wide_tiles_full).
 template <int WM, int WN>
 __global__ void __launch_bounds__(64 * WM * WN, 4)
 gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
                    const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                    const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
-                   uint16_t* __restrict__ act) {
+                   uint16_t* __restrict__ act, int both) {
   using P = G1TiledPaths<WM, WN>;
   // One LDS object: the stage ring, then the weight scale table.  (A second
   // __shared__ array makes the compiler wait for every outstanding LDS DMA
@@ -662,7 +678,8 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
   {
     ExpertRows X;
     X.load(expert_off);
-    tall_map = P::use_tall(X, gridDim.x);  // the same in every workgroup
+    if (both && wide_tiles_full(X)) return;  // the wide kernel takes this launch
+    tall_map = P::use_tall(X, gridDim.x);    // the same in every workgroup
   }
   const int xcd = blockIdx.x % 8, cap = gridDim.x / 8, slot = blockIdx.x / 8;
 #pragma unroll 1
@@ -694,7 +711,7 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
 
 template <int WM, int WN>
 hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
-                              const float* w13_scale, const Layout& L, char* ws, hipStream_t stream) {
+                              const float* w13_scale, const Layout& L, char* ws, hipStream_t stream, int both) {
   using P = G1TiledPaths<WM, WN>;
   const int64_t pairs = (int64_t)T * kTopK;
   const int64_t mtiles = (pairs + P::Short::BM - 1) / P::Short::BM + (pairs < kELocal ? pairs : kELocal);
@@ -705,7 +722,7 @@ hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, c
   const int64_t blocks = upper < cap ? upper : cap;
   hipLaunchKernelGGL((gemm1_tiled_kernel<WM, WN>), dim3((unsigned)blocks), dim3(P::kThreads), 0,
                      stream, hs, hs_scale, T, w13, w13_scale, (const int32_t*)(ws + L.expert_off),
-                     (const int32_t*)(ws + L.perm_token), (uint16_t*)(ws + L.act));
+                     (const int32_t*)(ws + L.perm_token), (uint16_t*)(ws + L.act), both);
   return hipGetLastError();
 }
 
@@ -754,16 +771,19 @@ struct G1Wide {
   static_assert(kStages * kStageBytes + kWscBytes <= 160 * 1024, "LDS");
 };
 
+// both: launched together with the tiled kernel; runs only if the row counts
+// choose the wide tiles (wide_tiles_full).
 __global__ void __launch_bounds__(G1Wide::kThreads)
 gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
                   const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                   const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
-                  uint16_t* __restrict__ act) {
+                  uint16_t* __restrict__ act, int both) {
   using C = G1Wide;
   __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
 
   ExpertRows X;
   X.load(expert_off);
+  if (both && !wide_tiles_full(X)) return;  // the tiled kernel takes this launch
   // An eighth of every expert's tiles per XCD (xcd_expert_tile): block b
   // takes tiles b / 8, b / 8 + cap, ... of XCD b % 8, cap being the blocks per
   // XCD.  The grid has a block per possible tile, so a block nearly always
@@ -983,14 +1003,14 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
 }
 
 hipError_t launch_gemm1_wide(const uint8_t* hs, const float* hs_scale, int T, const uint8_t* w13,
-                             const float* w13_scale, const Layout& L, char* ws, hipStream_t stream) {
+                             const float* w13_scale, const Layout& L, char* ws, hipStream_t stream, int both) {
   using C = G1Wide;
   const int64_t pairs = (int64_t)T * kTopK;
   const int64_t mtiles = (pairs + C::BM - 1) / C::BM + (pairs < kELocal ? pairs : kELocal);
   const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
   hipLaunchKernelGGL(gemm1_wide_kernel, dim3((unsigned)blocks), dim3(C::kThreads), 0, stream, hs, hs_scale, T,
                      w13, w13_scale, (const int32_t*)(ws + L.expert_off), (const int32_t*)(ws + L.perm_token),
-                     (uint16_t*)(ws + L.act));
+                     (uint16_t*)(ws + L.act), both);
   return hipGetLastError();
 }
 
@@ -1021,8 +1041,13 @@ hipError_t launch_gemm1(const uint8_t* hs, const float* hs_scale, int T, const u
     }
     return hipGetLastError();
   }
-  if (T < kGemm1TiledLargeMinTokens) return launch_gemm1_tiled<4, 2>(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
-  return launch_gemm1_wide(hs, hs_scale, T, w13, w13_scale, L, ws, stream);
+  if (T < kGemm1TiledLargeMinTokens) return launch_gemm1_tiled<4, 2>(hs, hs_scale, T, w13, w13_scale, L, ws, stream, 0);
+  if (T <= kGemm1BothMaxTokens) {
+    const hipError_t e = launch_gemm1_tiled<4, 2>(hs, hs_scale, T, w13, w13_scale, L, ws, stream, 1);
+    if (e != hipSuccess) return e;
+    return launch_gemm1_wide(hs, hs_scale, T, w13, w13_scale, L, ws, stream, 1);
+  }
+  return launch_gemm1_wide(hs, hs_scale, T, w13, w13_scale, L, ws, stream, 0);
 }
 
 }  // namespace moe

@@ -63,8 +63,12 @@ LAYER_CASES = [
     # hot expert; prefill routing with tall and short tiles
     ("skewed_t8192", None, 320, None),
     ("prefill_t1024", None, 704, None),
-    ("skewed_t8192", None, 1024, None),   # largest T of the tiled GEMM1
-    ("skewed_t8192", None, 1025, None),   # smallest T of the wide GEMM1
+    ("skewed_t8192", None, 1024, None),   # largest T of the tiled GEMM1 alone
+    # 1025 <= T <= 1536: both GEMM1 kernels launched, the row counts choose one
+    ("skewed_t8192", None, 1025, None),   # four hot experts: the wide kernel runs
+    ("prefill_t1024", None, 1025, None),  # rows spread: the tiled kernel runs
+    ("small_t64", None, 1536, None),      # the same at the range's top
+    ("prefill_t1024", None, 1537, None),  # the wide kernel alone
     ("skewed_t8192", None, 2047, None),
     ("skewed_t8192", None, 2048, None),
     ("skewed_t8192", None, 4095, None),
