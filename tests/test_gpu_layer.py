@@ -97,8 +97,9 @@ def test_layer_matches_oracle(pkg, orc, cuda_device, name, offset, T, n_check):
 
 
 # Other weights and tokens: generator seeds no config uses, each with another
-# local window and a T on another kernel path (streaming, tiled, wide GEMM1).
-SEED_CASES = [(5, 64, 50), (7, 160, 600), (9, 224, 1500)]
+# local window and a T on another kernel path (streaming, tiled with and
+# without tall tiles, the two-kernel range, wide GEMM1).
+SEED_CASES = [(5, 64, 50), (7, 160, 600), (9, 224, 1500), (11, 0, 800), (13, 96, 1100)]
 
 
 @pytest.mark.parametrize("seed,offset,T", SEED_CASES)
