@@ -527,7 +527,6 @@ __device__ __forceinline__ bool xcd_expert_tile(const ExpertRows& X, int x, int 
   return true;
 }
 
-
 // Row tiles of two heights: an expert's row tiles hold bm rows, its last one
 // fewer; a last row tile of at most bm / 2 rows is "short", every other row
 // tile "tall".  Totals over the experts (wave-level, uniform results).
