@@ -113,6 +113,20 @@ def test_layer_seed_sweep(pkg, orc, cuda_device, seed, offset, T):
     check_layer(pkg, orc, cuda_device, cfg, offset, tok, host, w, w_host, None)
 
 
+# A sweep over the tiled GEMM1's range and the two-kernel range (T = 65 to
+# 1,536 in steps of 122): tile maps with and without tall tiles, every token.
+SWEEP_CASES = [(name, T) for name in ("skewed_t8192", "prefill_t1024") for T in range(65, 1537, 122)]
+
+
+@pytest.mark.parametrize("name,T", SWEEP_CASES)
+def test_layer_sweep_mid_t(pkg, orc, cuda_device, name, T):
+    cfg = pkg.synth.CONFIGS[name]
+    w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, host = gpu_tokens(pkg, cfg, cuda_device, T)
+    print(f"layer sweep case {name} T={T}", flush=True)
+    check_layer(pkg, orc, cuda_device, cfg, cfg.local_expert_offset, tok, host, w, w_host, None)
+
+
 def check_layer(pkg, orc, cuda_device, cfg, off, tok, host, w, w_host, n_check):
     """Every checked token whose routed expert ids equal the oracle's is
     compared element-wise; a token whose ids differ must be a near-tie of the
