@@ -41,7 +41,13 @@ namespace {
 //     token gather is fused into the A load);
 //   * each wave copies its activation scales global -> LDS with
 //     global_load_lds_dword; the 8 K-partials are summed in LDS in a fixed
-//     order.
+//     order;
+//   * an expert of more than 16 rows (hot experts at 17 <= T <= 64) no longer
+//     fits one register tile: the loop would reload its rows per item.  The
+//     launch then runs the tiled kernel's tiles instead (gemm1_tiled_run, in
+//     this kernel's LDS at one workgroup per CU).  Interleaved A/B, GEMM1 us,
+//     four hot experts: T = 17 55.3 -> 38.4, 32 68.5 -> 38.9, 48 107.7 ->
+//     41.7, 64 173.8 -> 74.2; launches without such experts unchanged.
 // ---------------------------------------------------------------------------
 constexpr int kGemm1StreamMaxTokens = 64;
 constexpr int kGemm1DirectMaxTokens = 16;
@@ -52,6 +58,7 @@ constexpr int kS1Groups = kI / 8;         // 256 column groups per expert
 constexpr int kS1CopySplit = 4;           // weight copy parts: K blocks [0, 4) and [4, 7)
 constexpr int kS1CopyOps0 = 2 * kS1CopySplit;            // copies per lane, part 0
 constexpr int kS1CopyOps1 = 2 * (kS1KB - kS1CopySplit);  // copies per lane, part 1
+constexpr int kS1TiledLdsBytes = 80768;  // G1TiledPaths<4, 2>::kLdsBytes (checked where it is defined)
 
 // Operands of one 16-row tile that go out before it is multiplied.
 struct S1TileOps {
@@ -82,6 +89,13 @@ struct DirectRoute {
 };
 static_assert(kGemm1DirectMaxTokens == kSmallRouteMaxTokens, "the decode path routes in GEMM1");
 
+template <int WM, int WN>
+__device__ __forceinline__ void gemm1_tiled_run(char* lds, const uint8_t* __restrict__ hs,
+                                                const float* __restrict__ hs_scale, int T,
+                                                const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
+                                                const int32_t* __restrict__ expert_off,
+                                                const int32_t* __restrict__ perm_token, uint16_t* __restrict__ act);
+
 template <bool kDirect>
 __global__ void __launch_bounds__(kS1Threads)
 gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
@@ -100,6 +114,7 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
   constexpr int kPermOff = kInvOff + 16 * 4;
   constexpr int kSrOff = kPermOff + kTopK * kGemm1StreamMaxTokens * 4;  // kDirect: the routing
   constexpr int kLdsBytes = kSrOff + (kDirect ? (int)sizeof(SmallRoute) : 0);
+  static_assert(kLdsBytes >= kS1TiledLdsBytes, "the tiled tiles fit this kernel's LDS");
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
   float* red = (float*)(lds + kRedOff);
   int* inv = (int*)(lds + kInvOff);                  // kDirect: token -> permuted row, -1 if none
@@ -114,6 +129,15 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
   }
   ExpertRows X;
   X.load(eoff);
+  if constexpr (!kDirect) {
+    // An expert of more than 16 rows: its rows no longer fit one register
+    // tile and the streaming loop would reload them per item; run the tiled
+    // kernel's tiles instead (in this kernel's LDS, one workgroup per CU).
+    if (__ballot(X.cnt > 16) != 0 && gridDim.x % 8 == 0) {
+      gemm1_tiled_run<4, 2>(lds, hs, hs_scale, T, w13, w13_scale, expert_off, perm_token, act);
+      return;
+    }
+  }
   const uint32_t active = X.active();
   const int items = __popc(active) * kS1Groups;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -454,6 +478,7 @@ struct G1TiledPaths {
   static constexpr int kGroupM = 4;             // at most this many row tiles (of one expert) per L2 group
   static constexpr int kRingBytes = Short::kRingBytes > Tall::kRingBytes ? Short::kRingBytes : Tall::kRingBytes;
   static constexpr int kLdsBytes = kRingBytes + Short::kWscBytes;
+  static_assert(WM != 4 || WN != 2 || kLdsBytes <= kS1TiledLdsBytes, "the streaming kernel's LDS check");
   // Tall tiles (and the tall-first map) or short tiles only, for a grid of
   // `slots` resident workgroups.  In short-tile units a tall tile costs 1.5,
   // so the work is W = 1.5 tall + short against S short tiles.  Tall tiles
@@ -651,19 +676,16 @@ __device__ __forceinline__ void gemm1_tile(char* lds, float* wsc, const uint8_t*
       }
 }
 
-// both: launched together with the wide kernel; runs only if the row counts
-// choose the tiled tiles (!wide_tiles_full).
+// The tiled kernel's tile loop, over the whole grid; also run by the
+// streaming kernel when an expert has more than 16 rows.  `lds` holds at
+// least G1TiledPaths::kLdsBytes; the grid must be a multiple of 8.
 template <int WM, int WN>
-__global__ void __launch_bounds__(64 * WM * WN, 4)
-gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
-                   const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
-                   const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
-                   uint16_t* __restrict__ act, int both) {
+__device__ __forceinline__ void gemm1_tiled_run(char* lds, const uint8_t* __restrict__ hs,
+                                                const float* __restrict__ hs_scale, int T,
+                                                const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
+                                                const int32_t* __restrict__ expert_off,
+                                                const int32_t* __restrict__ perm_token, uint16_t* __restrict__ act) {
   using P = G1TiledPaths<WM, WN>;
-  // One LDS object: the stage ring, then the weight scale table.  (A second
-  // __shared__ array makes the compiler wait for every outstanding LDS DMA
-  // before any LDS read, which would serialise the pipeline.)
-  __shared__ __attribute__((aligned(1024))) char lds[P::kLdsBytes];
   float* wsc = (float*)(lds + P::kRingBytes);  // [WN][2][56]
 
   // Persistent: the grid is at most what fits on the device at once; each
@@ -678,7 +700,6 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
   {
     ExpertRows X;
     X.load(expert_off);
-    if (both && wide_tiles_full(X)) return;  // the wide kernel takes this launch
     tall_map = P::use_tall(X, gridDim.x);    // the same in every workgroup
   }
   const int xcd = blockIdx.x % 8, cap = gridDim.x / 8, slot = blockIdx.x / 8;
@@ -707,6 +728,29 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
       gemm1_tile<typename P::Short>(lds, wsc, hs, hs_scale, T, w13, w13_scale, perm_token, act, e, row0, rows, j0,
                                     w_once);
   }
+}
+
+
+// both: launched together with the wide kernel; runs only if the row counts
+// choose the tiled tiles (!wide_tiles_full).
+template <int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN, 4)
+gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
+                   const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
+                   const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
+                   uint16_t* __restrict__ act, int both) {
+  using P = G1TiledPaths<WM, WN>;
+  // One LDS object: the stage ring, then the weight scale table.  (A second
+  // __shared__ array makes the compiler wait for every outstanding LDS DMA
+  // before any LDS read, which would serialise the pipeline.)
+  __shared__ __attribute__((aligned(1024))) char lds[P::kLdsBytes];
+  float* wsc = (float*)(lds + P::kRingBytes);  // [WN][2][56]
+  {
+    ExpertRows X;
+    X.load(expert_off);
+    if (both && wide_tiles_full(X)) return;  // the wide kernel takes this launch
+  }
+  gemm1_tiled_run<WM, WN>(lds, hs, hs_scale, T, w13, w13_scale, expert_off, perm_token, act);
 }
 
 template <int WM, int WN>

@@ -54,8 +54,9 @@ LAYER_CASES = [
     ("skewed_t8192", None, 9, None),
     ("small_t64", None, 24, None),        # largest T of the one-workgroup routing launch
     ("small_t64", None, 25, None),        # routing plus a permutation launch
-    # streaming kernels with experts of more than 16 rows (four hot experts of
-    # up to 64 and 40 rows: the row-tile loops)
+    # experts of more than 16 rows at T <= 64 (four hot experts of T rows):
+    # the streaming GEMM1 launch runs the tiled kernel's tiles
+    ("skewed_t8192", None, 17, None),
     ("skewed_t8192", None, 64, None),
     ("skewed_t8192", None, 40, None),
     ("prefill_t1024", None, 65, None),    # first T with the tiled GEMM1 and a combine pass
@@ -176,7 +177,7 @@ def test_layer_matches_reference_golden(pkg, cuda_device, name):
 
 INTERMEDIATE_CASES = [
     ("small_t64", None, None),          # row-streaming kernels
-    ("skewed_t8192", 64, None),         # row-streaming kernels, experts of up to 64 rows
+    ("skewed_t8192", 64, None),         # streaming GEMM1 launch with tiled tiles (experts of 64 rows)
     ("prefill_t1024", None, 200),
     ("skewed_t8192", 2304, 160),        # LDS-tiled / wide kernels, ragged last tiles
     # tiled GEMM2 with experts of a few to ~40 rows, every row: 16-row blocks
