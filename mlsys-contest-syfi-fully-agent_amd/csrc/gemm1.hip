@@ -33,7 +33,8 @@ namespace {
 //     spreads over 256 workgroups and SwiGLU is one xor-8 lane exchange;
 //   * its 8 waves split K (7 scale blocks each) and issue all their weight
 //     loads before the first MFMA; every 16-row tile of the expert's tokens
-//     reuses them from registers;
+//     reuses them from registers (more than one tile per expert only on the
+//     fallback below, a grid that is not a multiple of 8);
 //   * kDirect (T <= 16): the MFMA rows are the T tokens themselves, so the
 //     activation loads need no permutation lookup and go out together with
 //     the weight loads; results are written to the permuted rows of the
