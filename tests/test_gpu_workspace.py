@@ -87,3 +87,37 @@ def test_captured_workspace_outlives_growth(pkg, cuda_device):
         del junk
     del graph
     pkg.release_workspaces()
+
+
+@pytest.mark.parametrize("name,T", [("small_t64", 1100), ("skewed_t8192", 1025)])
+def test_graph_replay_with_both_gemm1_kernels(pkg, cuda_device, name, T):
+    """For 1,025-1,536 tokens the layer launches both GEMM1 kernels and the
+    row counts choose one (the tiled kernel for spread rows, the wide one for
+    hot experts).  A graph of such a call replays to the eager bits, with
+    eager work between the replays."""
+    cfg = pkg.synth.CONFIGS[name]
+    w, _ = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, _ = gpu_tokens(pkg, cfg, cuda_device, T)
+    print(f"graph case {name} T={T}", flush=True)
+    ref = _out(T, cuda_device)
+    pkg.run(*tok, *w, cfg.local_expert_offset, cfg.routed_scaling_factor, ref)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream(device=cuda_device)
+    got = _out(T, cuda_device)
+    with torch.cuda.stream(s):
+        pkg.run(*tok, *w, cfg.local_expert_offset, cfg.routed_scaling_factor, got)  # eager warm-up on s
+    s.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        pkg.run(*tok, *w, cfg.local_expert_offset, cfg.routed_scaling_factor, got)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        got.fill_(float("nan"))
+        junk = torch.full((1 << 20,), 3, dtype=torch.int32, device=cuda_device)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), f"replay {rep}"
+        del junk
+    del graph
+    pkg.release_workspaces()
