@@ -161,18 +161,32 @@ __device__ __forceinline__ v4i s2_op(const S2Regs& R, int k, int g, int h, int p
 // -> the wave's LDS stage: per 16-row block and K block two wide planes (rows
 // 0-7, 8-15), 128 bytes per row, chunks swizzled, so every copy reads 8 whole
 // 128-byte row segments.  8 copies per lane.
-__device__ __forceinline__ void s2_copy_w(char* stage, S2Job j, const uint8_t* __restrict__ w2, int n0, int kb0,
-                                          int lane) {
+__device__ __forceinline__ void s2_copy_w(char* stage, S2Job j, const ExpertRows& X, const uint8_t* __restrict__ w2,
+                                          int n0, int kb0, int lane) {
+  auto copy = [&](auto nt_c) {
 #pragma unroll
-  for (int nb = 0; nb < kS2NB; ++nb)
+    for (int nb = 0; nb < kS2NB; ++nb)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      int r, c;
-      wide_copy_lane(lane, h, r, c);
-      const uint8_t* src = w2 + ((size_t)j.e * kH + n0 + 16 * nb + r) * kI + kb0 * kBlk + 16 * c;
+      for (int h = 0; h < 2; ++h) {
+        int r, c;
+        wide_copy_lane(lane, h, r, c);
+        const uint8_t* src = w2 + ((size_t)j.e * kH + n0 + 16 * nb + r) * kI + kb0 * kBlk + 16 * c;
 #pragma unroll
-      for (int k = 0; k < kS2KB; ++k) dma16_nt(src + k * kBlk, stage + ((nb * kS2KB + k) * 2 + h) * 1024);
-    }
+        for (int k = 0; k < kS2KB; ++k) {
+          if constexpr (decltype(nt_c)::value)
+            dma16_nt(src + k * kBlk, stage + ((nb * kS2KB + k) * 2 + h) * 1024);
+          else
+            dma16(src + k * kBlk, stage + ((nb * kS2KB + k) * 2 + h) * 1024);
+        }
+      }
+  };
+  // A row tile with more of the expert's row tiles after it: the next job
+  // copies the same W2 slice again, so the lines stay in L2 for it; the
+  // expert's last row tile reads them for the last time.
+  if ((j.rt + 1) * 16 < X.end(j.e) - X.begin(j.e))
+    copy(std::false_type{});
+  else
+    copy(std::true_type{});
 }
 
 __global__ void __launch_bounds__(kS2Threads)
@@ -227,8 +241,8 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
     S2Regs r0, r1;
     if (job.e >= 0) {
       s2_load<S>(r0, job, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
-      s2_copy_w(stage(0), job, w2, n0, kb0, lane);
-      s2_copy_w(stage(1), j1.e >= 0 ? j1 : job, w2, n0, kb0, lane);
+      s2_copy_w(stage(0), job, X, w2, n0, kb0, lane);
+      s2_copy_w(stage(1), j1.e >= 0 ? j1 : job, X, w2, n0, kb0, lane);
     }
     // One job from stage `s` with act rows `cur`; after its MFMAs, loads the
     // next job's act rows into `nxt` and starts the copy of the job after next
@@ -275,7 +289,7 @@ gemm2_combine_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict
       // (small_t64 GEMM2 62.5 -> 61.5 us).
       if (j1.e >= 0) {
         s2_load<S>(nxt, j1, X, perm_token, perm_w, act, w2_scale, n0, kb0, lq, lr);
-        s2_copy_w(stage(s), j2.e >= 0 ? j2 : j1, w2, n0, kb0, lane);
+        s2_copy_w(stage(s), j2.e >= 0 ? j2 : j1, X, w2, n0, kb0, lane);
       }
       lds_barrier();
       {
