@@ -459,9 +459,11 @@ struct G1Tiled {
 
 // Two tile heights.  Short tiles hold up to 64 rows of one expert (one 16-row
 // block per wave, a 3-stage ring); tall tiles 65-128 rows (two blocks per
-// wave, a 2-stage ring), so the W13 columns of those rows pass through the
-// copy path once instead of once per 64 rows -- the copy path (about 9.5 TB/s
-// of L2 -> LDS over the chip), not HBM, bounds this kernel.  Rows past a
+// wave, a 2-stage ring), so the W13 columns of those rows are copied (and,
+// for an expert of up to 128 rows, read from HBM) once instead of once per 64
+// rows.  The kernel waits on that weight stream: with every tile's W13
+// L2-resident (a timing-only copy) it ran 26 % faster at T = 1024, while more
+// lookahead through L2 prefetches made it slower.  Rows past a
 // tile's last row copy its last row again, which costs the copy path nothing
 // (lanes given an out-of-range buffer offset instead changed no time).  Both
 // rings fit one LDS array of the short ring's size: two workgroups per CU.
