@@ -128,24 +128,48 @@ def test_layer_sweep_mid_t(pkg, orc, cuda_device, name, T):
     check_layer(pkg, orc, cuda_device, cfg, cfg.local_expert_offset, tok, host, w, w_host, None)
 
 
-def check_layer(pkg, orc, cuda_device, cfg, off, tok, host, w, w_host, n_check):
+# Routed scaling factors other than the configurations' 2.5 (the definition
+# takes any value, moe.py:158): the factor passes through every routing
+# implementation -- inside GEMM1 (T <= 16), the one-workgroup routing launch
+# (T <= 24) and the routing kernel with its permutation launch -- and scales
+# every output row, so a factor dropped or applied twice on any path fails.
+RSF_CASES = [
+    ("decode_t1_s3", 1.0, None),
+    ("plumbing_t16", 0.37, None),
+    ("small_t64", 7.0, 20),
+    ("prefill_t1024", 1.0, 300),
+    ("skewed_t8192", 0.125, 1500),
+]
+
+
+@pytest.mark.parametrize("name,rsf,T", RSF_CASES)
+def test_layer_other_scaling_factors(pkg, orc, cuda_device, name, rsf, T):
+    cfg = pkg.synth.CONFIGS[name]
+    w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, host = gpu_tokens(pkg, cfg, cuda_device, T)
+    print(f"layer rsf case {name} rsf={rsf} T={tok[0].shape[0]}", flush=True)
+    check_layer(pkg, orc, cuda_device, cfg, cfg.local_expert_offset, tok, host, w, w_host, None, rsf=rsf)
+
+
+def check_layer(pkg, orc, cuda_device, cfg, off, tok, host, w, w_host, n_check, rsf=None):
     """Every checked token whose routed expert ids equal the oracle's is
     compared element-wise; a token whose ids differ must be a near-tie of the
     fp32 scores (and is then left out)."""
     T = tok[0].shape[0]
-    out = run_layer(pkg, tok, w, off, cfg.routed_scaling_factor).float().cpu().numpy()
+    rsf = cfg.routed_scaling_factor if rsf is None else rsf
+    out = run_layer(pkg, tok, w, off, rsf).float().cpu().numpy()
     assert np.isfinite(out).all(), "output not fully written / non-finite"
     gpu_ids = pkg.intermediates(pkg.workspace(cuda_device, T), T).topk_ids.cpu().numpy()
 
-    ref_ids, _ = orc.route(host[0], host[1], cfg.routed_scaling_factor)
-    tie = near_tie_tokens(host[0], host[1], cfg.routed_scaling_factor)
+    ref_ids, _ = orc.route(host[0], host[1], rsf)
+    tie = near_tie_tokens(host[0], host[1], rsf)
     differ = (np.sort(gpu_ids, axis=1) != ref_ids).any(axis=1)
     assert not (differ & ~tie).any(), f"ids differ outside near-ties: tokens {np.nonzero(differ & ~tie)[0][:8]}"
     rng = np.random.default_rng(T)
     toks = np.arange(T) if n_check is None or T <= n_check else sample_tokens(ref_ids, off, n_check, rng, T)
     toks = toks[~differ[toks]]
     x = oracle_inputs(cfg, host, w_host)
-    ref = orc.bf16_to_f32(orc.moe(x, tokens=toks, local_expert_offset=off))
+    ref = orc.bf16_to_f32(orc.moe(x, tokens=toks, local_expert_offset=off, rsf=rsf))
     got = out[toks]
     bad = bf16_close(got, ref)
     err = np.abs(got - ref)

@@ -69,6 +69,21 @@ def test_route_seed_sweep(pkg, orc, cuda_device, seed, offset):
     check_route(pkg, orc, tok, host, offset, cfg.routed_scaling_factor)
 
 
+# Other routed scaling factors on each routing implementation: T = 1 and 16
+# (single-token and one-workgroup paths), 24 / 25 (either side of the
+# one-launch limit) and 300 (route kernel + permutation).
+RSF_ROUTE_CASES = [(T, rsf) for T in (1, 16, 24, 25, 300) for rsf in (1.0, 0.37, 7.0)]
+
+
+@pytest.mark.parametrize("T,rsf", RSF_ROUTE_CASES)
+def test_route_other_scaling_factors(pkg, orc, cuda_device, T, rsf):
+    cfg = pkg.synth.CONFIGS["prefill_t1024"]
+    tok = pkg.synth.tokens(cfg, cuda_device, T)
+    host = (tok[0].cpu().numpy(), tok[1].view(torch.int16).cpu().numpy().view(np.uint16))
+    print(f"route rsf case T={T} rsf={rsf}", flush=True)
+    check_route(pkg, orc, tok, host, cfg.local_expert_offset, rsf)
+
+
 def check_route(pkg, orc, tok, host, off, rsf):
     """Expert ids equal the oracle's (moe.py:123-158) outside near-ties of the
     fp32 scores, weights bit-exact where the ids agree, and the permutation is
