@@ -151,6 +151,35 @@ def test_layer_other_scaling_factors(pkg, orc, cuda_device, name, rsf, T):
     check_layer(pkg, orc, cuda_device, cfg, cfg.local_expert_offset, tok, host, w, w_host, None, rsf=rsf)
 
 
+# Every selection local (N_sel = 8 T, the largest row count the workspace
+# holds): +10 on the bias of the 32 local experts puts their group first and
+# all 8 picks in it, for every token, so the experts hold about T / 4 rows
+# each -- experts of more than 16 rows in the streaming kernels at T = 64,
+# tall tiles at T = 300, the two-kernel range (the wide tiles chosen) at
+# T = 1100 and the wide GEMM1 alone at T = 3000.
+ALL_LOCAL_CASES = [(1, None), (16, None), (64, None), (300, None), (1100, 256), (3000, 256)]
+
+
+@pytest.mark.parametrize("T,n_check", ALL_LOCAL_CASES)
+def test_layer_every_selection_local(pkg, orc, cuda_device, T, n_check):
+    cfg = pkg.synth.CONFIGS["prefill_t1024"]
+    off = cfg.local_expert_offset
+    w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, host = gpu_tokens(pkg, cfg, cuda_device, T)
+    bias = tok[1].float()
+    bias[off:off + 32] += 10.0
+    bias = bias.to(torch.bfloat16)
+    tok = (tok[0], bias, tok[2], tok[3])
+    host = (host[0], bias.view(torch.int16).cpu().numpy().view(np.uint16), host[2], host[3])
+    ref_ids, _ = orc.route(host[0], host[1], cfg.routed_scaling_factor)
+    assert ((ref_ids >= off) & (ref_ids < off + 32)).all(), "every pick local"
+    print(f"layer every-selection-local case T={T}", flush=True)
+    check_layer(pkg, orc, cuda_device, cfg, off, tok, host, w, w_host, n_check)
+    if T > 16:  # the routing launches write the row offsets (at T <= 16 GEMM1 routes)
+        offs = pkg.intermediates(pkg.workspace(cuda_device, T), T).expert_off.cpu().numpy()
+        assert offs[32] == 8 * T and (np.diff(offs) >= 0).all()
+
+
 def check_layer(pkg, orc, cuda_device, cfg, off, tok, host, w, w_host, n_check, rsf=None):
     """Every checked token whose routed expert ids equal the oracle's is
     compared element-wise; a token whose ids differ must be a near-tie of the
