@@ -84,6 +84,10 @@ LAYER_CASES = [
     ("prefill_t1024", 128, 777, None),
     ("prefill_t1024", 32, 1537, None),
     ("prefill_t1024", 224, 3001, None),
+    # windows that start inside a routing group (any offset is allowed)
+    ("prefill_t1024", 77, 100, None),
+    ("small_t64", 5, 64, None),
+    ("skewed_t8192", 13, 2100, 384),
 ]
 
 
