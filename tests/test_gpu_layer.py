@@ -184,6 +184,33 @@ def test_layer_every_selection_local(pkg, orc, cuda_device, T, n_check):
         assert offs[32] == 8 * T and (np.diff(offs) >= 0).all()
 
 
+def _random_cases(n, seed):
+    """(routing config, T, window offset, token seed, weight seed, rsf) drawn
+    from a fixed generator: T over every kernel path, any window start in
+    [-31, 256), token seeds no configuration uses."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        name = ("prefill_t1024", "skewed_t8192", "small_t64")[int(rng.integers(3))]
+        r = rng.random()
+        T = int(rng.integers(1, 65)) if r < 0.35 else int(rng.integers(65, 1600)) if r < 0.8 else int(rng.integers(1600, 5000))
+        out.append((name, T, int(rng.integers(-31, 256)), int(rng.integers(30, 60)),
+                    None if rng.random() < 0.7 else int(rng.integers(30, 40)), float(rng.choice([2.5, 1.0, 0.5, 3.7]))))
+    # grouped by weights, which the test helpers keep one seed of at a time
+    return sorted(out, key=lambda c: (c[4] is None, c[4] or 0, c[0]))
+
+
+@pytest.mark.parametrize("name,T,offset,seed,wseed,rsf", _random_cases(40, 2024))
+def test_layer_random_cases(pkg, orc, cuda_device, name, T, offset, seed, wseed, rsf):
+    cfg = pkg.synth.CONFIGS[name]
+    w, w_host = gpu_weights(pkg, cfg.seed if wseed is None else wseed, cuda_device)
+    tok = pkg.synth.tokens(cfg, cuda_device, T, seed=seed)
+    host = (tok[0].cpu().numpy(), tok[1].view(torch.int16).cpu().numpy().view(np.uint16),
+            tok[2].view(torch.uint8).cpu().numpy(), tok[3].cpu().numpy())
+    print(f"layer random case {name} T={T} offset={offset} seed={seed} wseed={wseed} rsf={rsf}", flush=True)
+    check_layer(pkg, orc, cuda_device, cfg, offset, tok, host, w, w_host, None if T <= 256 else 96, rsf=rsf)
+
+
 def check_layer(pkg, orc, cuda_device, cfg, off, tok, host, w, w_host, n_check, rsf=None):
     """Every checked token whose routed expert ids equal the oracle's is
     compared element-wise; a token whose ids differ must be a near-tie of the
