@@ -140,9 +140,14 @@ typedef struct {
   size_t perm_token; /* int32 [8T]     token of each permuted row                 */
   size_t perm_w;     /* float [8T]     combination weight of each permuted row    */
   size_t act;        /* bf16 pairs [8T, 4096]: SwiGLU output rows, value = hi + lo;
-                        per 64-column chunk c, 64 hi then 64 lo bf16 (8 KB/row)   */
+                        per 64-column chunk c, 64 hi then 64 lo bf16 (8 KB/row).
+                        T >= 1024 with two or more local experts that every token
+                        selects: their rows times the routing weight              */
   size_t down;       /* float [8T, 7168] GEMM2 output rows (T > 64 only; for
-                        T <= 64 GEMM2 combines in registers and the region is empty) */
+                        T <= 64 GEMM2 combines in registers and the region is empty).
+                        Experts every token selects (as for act): the first one's
+                        rows hold each token's weighted sum over all of them, the
+                        others' rows are not written                              */
   size_t block_hist; /* int32 [workgroups, 32] local-expert pairs per routing workgroup
                         (T > 16; ceil(T/4) workgroups up to T = 1024, ceil(T/16) beyond) */
   size_t total;      /* = moe_fp8_ds_workspace_size(T)                            */

@@ -33,7 +33,8 @@ static_assert(kCombParts * kCombCols == kH && kCombThreads % kWave == 0, "whole 
 
 __global__ void __launch_bounds__(kCombThreads)
 combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_row,
-               const float* __restrict__ topk_w, uint16_t* __restrict__ out) {
+               const float* __restrict__ topk_w, const int32_t* __restrict__ expert_off, int T,
+               uint16_t* __restrict__ out) {
   const int t = blockIdx.x / kCombParts;
   const int c0 = (blockIdx.x % kCombParts) * kCombCols + (int)threadIdx.x * 4;
   const int c[2] = {c0, c0 + kCombCols / 2};
@@ -43,6 +44,25 @@ combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_
   for (int k = 0; k < kTopK; ++k) {
     row[k] = pair_row[(size_t)t * kTopK + k];
     w[k] = topk_w[(size_t)t * kTopK + k];
+  }
+  // Experts of every token (every_token_experts): GEMM2 wrote the token's
+  // weighted sum over them to the first one's row; add that row once, with
+  // weight 1, at its place in expert order, and skip the others' rows.
+  ExpertRows X;
+  X.load(expert_off);
+  const uint32_t fused = every_token_experts(X, T);
+  if (fused) {
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+      if (row[k] < 0) continue;  // token-uniform
+      const int e = expert_of_row(X, row[k]);
+      if ((fused >> e) & 1u) {
+        if (e == __builtin_ctz(fused))
+          w[k] = 1.0f;
+        else
+          row[k] = -1;
+      }
+    }
   }
   v4f v[kTopK][2];
 #pragma unroll
@@ -77,7 +97,7 @@ combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_
 hipError_t launch_combine(int T, const Layout& L, char* ws, void* out, hipStream_t stream) {
   hipLaunchKernelGGL(combine_kernel, dim3(T * kCombParts), dim3(kCombThreads), 0, stream,
                      (const float*)(ws + L.down), (const int32_t*)(ws + L.pair_row),
-                     (const float*)(ws + L.topk_w), (uint16_t*)out);
+                     (const float*)(ws + L.topk_w), (const int32_t*)(ws + L.expert_off), T, (uint16_t*)out);
   return hipGetLastError();
 }
 

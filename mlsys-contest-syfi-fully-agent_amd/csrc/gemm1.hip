@@ -59,7 +59,7 @@ constexpr int kS1Groups = kI / 8;         // 256 column groups per expert
 constexpr int kS1CopySplit = 4;           // weight copy parts: K blocks [0, 4) and [4, 7)
 constexpr int kS1CopyOps0 = 2 * kS1CopySplit;            // copies per lane, part 0
 constexpr int kS1CopyOps1 = 2 * (kS1KB - kS1CopySplit);  // copies per lane, part 1
-constexpr int kS1TiledLdsBytes = 80768;  // G1TiledPaths<4, 2>::kLdsBytes (checked where it is defined)
+constexpr int kS1TiledLdsBytes = 81280;  // G1TiledPaths<4, 2>::kLdsBytes (checked where it is defined)
 
 // Operands of one 16-row tile that go out before it is multiplied.
 struct S1TileOps {
@@ -95,7 +95,8 @@ __device__ __forceinline__ void gemm1_tiled_run(char* lds, const uint8_t* __rest
                                                 const float* __restrict__ hs_scale, int T,
                                                 const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                                                 const int32_t* __restrict__ expert_off,
-                                                const int32_t* __restrict__ perm_token, uint16_t* __restrict__ act);
+                                                const int32_t* __restrict__ perm_token, const float* __restrict__ perm_w,
+                                                uint16_t* __restrict__ act);
 
 template <bool kDirect>
 __global__ void __launch_bounds__(kS1Threads)
@@ -135,7 +136,7 @@ gemm1_stream_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs
     // tile and the streaming loop would reload them per item; run the tiled
     // kernel's tiles instead (in this kernel's LDS, one workgroup per CU).
     if (__ballot(X.cnt > 16) != 0 && gridDim.x % 8 == 0) {
-      gemm1_tiled_run<4, 2>(lds, hs, hs_scale, T, w13, w13_scale, expert_off, perm_token, act);
+      gemm1_tiled_run<4, 2>(lds, hs, hs_scale, T, w13, w13_scale, expert_off, perm_token, nullptr, act);
       return;
     }
   }
@@ -480,7 +481,8 @@ struct G1TiledPaths {
   static constexpr int kThreads = Short::kThreads;
   static constexpr int kGroupM = 4;             // at most this many row tiles (of one expert) per L2 group
   static constexpr int kRingBytes = Short::kRingBytes > Tall::kRingBytes ? Short::kRingBytes : Tall::kRingBytes;
-  static constexpr int kLdsBytes = kRingBytes + Short::kWscBytes;
+  static constexpr int kRowWBytes = Tall::BM * 4;  // the tile's routing weights (every_token_experts)
+  static constexpr int kLdsBytes = kRingBytes + Short::kWscBytes + kRowWBytes;
   static_assert(WM != 4 || WN != 2 || kLdsBytes <= kS1TiledLdsBytes, "the streaming kernel's LDS check");
   // Tall tiles (and the tall-first map) or short tiles only, for a grid of
   // `slots` resident workgroups.  In short-tile units a tall tile costs 1.5,
@@ -517,7 +519,8 @@ __device__ __forceinline__ void gemm1_tile(char* lds, float* wsc, const uint8_t*
                                            const float* __restrict__ hs_scale, int T,
                                            const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                                            const int32_t* __restrict__ perm_token, uint16_t* __restrict__ act,
-                                           int e, int row0, int rows, int j0, bool w_once) {
+                                           int e, int row0, int rows, int j0, bool w_once,
+                                           const float* __restrict__ perm_w, bool fold_w) {
   constexpr int WN = C::kWN, MI = C::kMI;
   // The thread index is opaque to the optimiser: values derived from it are
   // computed per tile, not hoisted out of the tile loop and kept live
@@ -588,6 +591,10 @@ __device__ __forceinline__ void gemm1_tile(char* lds, float* wsc, const uint8_t*
     const int blk = (up ? kI : 0) + j0 + 32 * w_n;
     wsc[i] = w13_scale[((size_t)e * kN2IBlk + blk / kBlk) * kNHBlk + kb];
   }
+  // the rows' routing weights, for the epilogue (every_token_experts)
+  float* roww = wsc + WN * 2 * kNHBlk;
+  if (fold_w)
+    for (int i = tid; i < rows; i += C::kThreads) roww[i] = perm_w[row0 + i];
 
   v4f acc[MI][4];
 #pragma unroll
@@ -670,8 +677,10 @@ __device__ __forceinline__ void gemm1_tile(char* lds, float* wsc, const uint8_t*
         const int r = (wm * MI + mi) * 16 + 4 * lq + i;
         if (r < rows) {
           const float x1 = acc[mi][nj][i], x2 = acc[mi][nj + 2][i];
+          float v = silu_mul(x2, x1);
+          if (fold_w) v = v * roww[r];  // every_token_experts: the routing weight
           uint16_t hi, lo;
-          split_bf16(silu_mul(x2, x1), hi, lo);
+          split_bf16(v, hi, lo);
           uint16_t* p = act + (size_t)(row0 + r) * kActRowElems + act_col(j0 + 32 * wn + 16 * nj + lr);
           p[0] = hi;
           p[64] = lo;
@@ -687,7 +696,8 @@ __device__ __forceinline__ void gemm1_tiled_run(char* lds, const uint8_t* __rest
                                                 const float* __restrict__ hs_scale, int T,
                                                 const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                                                 const int32_t* __restrict__ expert_off,
-                                                const int32_t* __restrict__ perm_token, uint16_t* __restrict__ act) {
+                                                const int32_t* __restrict__ perm_token, const float* __restrict__ perm_w,
+                                                uint16_t* __restrict__ act) {
   using P = G1TiledPaths<WM, WN>;
   float* wsc = (float*)(lds + P::kRingBytes);  // [WN][2][56]
 
@@ -724,12 +734,13 @@ __device__ __forceinline__ void gemm1_tiled_run(char* lds, const uint8_t* __rest
     if (it > 0) block_barrier();  // every wave is done with the previous tile's LDS
     const int j0 = nt * P::Short::kGateCols;
     const bool w_once = X.end(e) - X.begin(e) <= (tall_map ? P::BM : P::Short::BM);  // one row tile
+    const bool fold_w = (every_token_experts(X, T) >> e) & 1u;
     if (rows > P::Short::BM)  // workgroup-uniform
       gemm1_tile<typename P::Tall>(lds, wsc, hs, hs_scale, T, w13, w13_scale, perm_token, act, e, row0, rows, j0,
-                                   w_once);
+                                   w_once, perm_w, fold_w);
     else
       gemm1_tile<typename P::Short>(lds, wsc, hs, hs_scale, T, w13, w13_scale, perm_token, act, e, row0, rows, j0,
-                                    w_once);
+                                    w_once, perm_w, fold_w);
   }
 }
 
@@ -741,7 +752,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 4)
 gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
                    const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                    const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
-                   uint16_t* __restrict__ act, int both) {
+                   const float* __restrict__ perm_w, uint16_t* __restrict__ act, int both) {
   using P = G1TiledPaths<WM, WN>;
   // One LDS object: the stage ring, then the weight scale table.  (A second
   // __shared__ array makes the compiler wait for every outstanding LDS DMA
@@ -753,7 +764,7 @@ gemm1_tiled_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_
     X.load(expert_off);
     if (both && wide_tiles_full(X)) return;  // the wide kernel takes this launch
   }
-  gemm1_tiled_run<WM, WN>(lds, hs, hs_scale, T, w13, w13_scale, expert_off, perm_token, act);
+  gemm1_tiled_run<WM, WN>(lds, hs, hs_scale, T, w13, w13_scale, expert_off, perm_token, perm_w, act);
 }
 
 template <int WM, int WN>
@@ -769,7 +780,8 @@ hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, c
   const int64_t blocks = upper < cap ? upper : cap;
   hipLaunchKernelGGL((gemm1_tiled_kernel<WM, WN>), dim3((unsigned)blocks), dim3(P::kThreads), 0,
                      stream, hs, hs_scale, T, w13, w13_scale, (const int32_t*)(ws + L.expert_off),
-                     (const int32_t*)(ws + L.perm_token), (uint16_t*)(ws + L.act), both);
+                     (const int32_t*)(ws + L.perm_token), (const float*)(ws + L.perm_w), (uint16_t*)(ws + L.act),
+                     both);
   return hipGetLastError();
 }
 
@@ -824,13 +836,14 @@ __global__ void __launch_bounds__(G1Wide::kThreads)
 gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_scale, int T,
                   const uint8_t* __restrict__ w13, const float* __restrict__ w13_scale,
                   const int32_t* __restrict__ expert_off, const int32_t* __restrict__ perm_token,
-                  uint16_t* __restrict__ act, int both) {
+                  const float* __restrict__ perm_w, uint16_t* __restrict__ act, int both) {
   using C = G1Wide;
   __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
 
   ExpertRows X;
   X.load(expert_off);
   if (both && !wide_tiles_full(X)) return;  // the tiled kernel takes this launch
+  const uint32_t fused = every_token_experts(X, T);
   // An eighth of every expert's tiles per XCD (xcd_expert_tile): block b
   // takes tiles b / 8, b / 8 + cap, ... of XCD b % 8, cap being the blocks per
   // XCD.  The grid has a block per possible tile, so a block nearly always
@@ -1032,11 +1045,17 @@ gemm1_wide_kernel(const uint8_t* __restrict__ hs, const float* __restrict__ hs_s
     if (r < rows) {
       uint16_t* arow = act + (size_t)(row0 + r) * kActRowElems;
       const int c0 = j0 + 16 * C::NJ * wn + 4 * lq;  // 4 adjacent columns: one 8-byte store per half
+      // every_token_experts: the row's routing weight folded in
+      const float wr = (fused >> e) & 1u ? perm_w[row0 + r] : 1.0f;
 #pragma unroll
       for (int nj = 0; nj < C::NJ; ++nj) {
         float c[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) c[i] = silu_mul(acc[mi][C::NJ + nj][i], acc[mi][nj][i]);
+        if ((fused >> e) & 1u) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) c[i] = c[i] * wr;
+        }
         uint2 h, l;
         split_bf16x2(c[0], c[1], h.x, l.x);
         split_bf16x2(c[2], c[3], h.y, l.y);
@@ -1057,7 +1076,7 @@ hipError_t launch_gemm1_wide(const uint8_t* hs, const float* hs_scale, int T, co
   const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
   hipLaunchKernelGGL(gemm1_wide_kernel, dim3((unsigned)blocks), dim3(C::kThreads), 0, stream, hs, hs_scale, T,
                      w13, w13_scale, (const int32_t*)(ws + L.expert_off), (const int32_t*)(ws + L.perm_token),
-                     (uint16_t*)(ws + L.act), both);
+                     (const float*)(ws + L.perm_w), (uint16_t*)(ws + L.act), both);
   return hipGetLastError();
 }
 

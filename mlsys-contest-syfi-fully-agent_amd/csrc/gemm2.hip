@@ -373,7 +373,7 @@ struct G2Tiled {
   static constexpr int kBFrags = BN / 16;
   static constexpr int kBOff = kAFrags * kAFragBytes;
   static constexpr int kStageBytes = kBOff + kBFrags * 1024;
-  static constexpr int kWscBytes = WN * kNIBlk * 4;  // weight block scales (after the stages)
+  static constexpr int kWscBytes = kTopK * WN * kNIBlk * 4;  // weight block scales of up to 8 experts (after the stages)
   static constexpr int kStages = STAGES;
   static_assert(kStages >= 2 && kStages <= 5, "pipeline depth");
   static constexpr int kSteps = kI / 64;  // stages per tile (two per scale block)
@@ -387,20 +387,58 @@ template <int WM, int WN, int MI, int NJ, int STAGES>
 __global__ void __launch_bounds__(64 * WM * WN, 4)
 gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w2,
                    const float* __restrict__ w2_scale, const int32_t* __restrict__ expert_off,
-                   float* __restrict__ down) {
+                   float* __restrict__ down, int T) {
   using C = G2Tiled<WM, WN, MI, NJ, STAGES>;
   // One LDS object (see gemm1.hip): the stage ring, then the weight scales.
   __shared__ __attribute__((aligned(1024))) char lds[C::kStages * C::kStageBytes + C::kWscBytes];
 
   ExpertRows X;
   X.load(expert_off);
-  const int mt_total = X.count_tiles(C::BM);
-  const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
-  if (t < 0) return;
-  int mt, nt;
-  grouped_tile(X, t, C::BM, C::kNT, C::kGroupM, mt, nt);
-  int e, row0, rows;
-  X.find_tile(mt, C::BM, e, row0, rows);
+  // Experts of every token (every_token_experts): a fused tile takes row tile
+  // mt of each of them (tokens 64 mt ..), runs its K loop over all of them in
+  // expert order into one accumulator (GEMM1 folded the routing weights into
+  // their rows) and writes the sum to the first one's rows.
+  const uint32_t fused = every_token_experts(X, T);
+  int mt, nt, e, row0, rows;
+  uint32_t tile_exps;  // the experts whose K loops this tile runs, in order
+  if (!fused) {
+    const int mt_total = X.count_tiles(C::BM);
+    const int t = xcd_tile(blockIdx.x, mt_total * C::kNT);
+    if (t < 0) return;
+    grouped_tile(X, t, C::BM, C::kNT, C::kGroupM, mt, nt);
+    X.find_tile(mt, C::BM, e, row0, rows);
+    tile_exps = 1u << e;
+  } else {
+    // XCD x = block % 8 takes the x-th eighth of the fused tiles (the long
+    // ones) first, then the x-th eighth of the other experts' tiles.
+    const int lane = threadIdx.x & (kWave - 1);
+    ExpertRows Xs = X;
+    if (lane < kELocal && ((fused >> lane) & 1u)) Xs.cnt = 0;
+    const int frt = (T + C::BM - 1) / C::BM;  // fused row tiles
+    const int nf = frt * C::kNT, ns = Xs.count_tiles(C::BM) * C::kNT;
+    const int x = blockIdx.x % 8, l = blockIdx.x / 8;
+    const int f0 = (int)((int64_t)x * nf / 8), f1 = (int)((int64_t)(x + 1) * nf / 8);
+    const int s0 = (int)((int64_t)x * ns / 8), s1 = (int)((int64_t)(x + 1) * ns / 8);
+    if (l < f1 - f0) {
+      // L2 groups of kGroupM row tiles sweeping the column tiles, row tile fastest
+      const int idx = f0 + l, per_group = C::kGroupM * C::kNT;
+      const int g = idx / per_group, within = idx % per_group;
+      const int size = min(C::kGroupM, frt - g * C::kGroupM);
+      mt = g * C::kGroupM + within % size;
+      nt = within / size;
+      e = __builtin_ctz(fused);
+      row0 = X.begin(e) + mt * C::BM;
+      rows = min(C::BM, T - mt * C::BM);
+      tile_exps = fused;
+    } else if (l - (f1 - f0) < s1 - s0) {
+      grouped_tile(Xs, s0 + l - (f1 - f0), C::BM, C::kNT, C::kGroupM, mt, nt);
+      Xs.find_tile(mt, C::BM, e, row0, rows);
+      tile_exps = 1u << e;
+    } else {
+      return;
+    }
+  }
+  const int n_steps = __builtin_popcount(tile_exps) * C::kSteps;
   const int n0 = nt * C::BN;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -422,8 +460,10 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
   // 1,646 -> 1,631 us, 128 -> 122 VGPRs).
   static_assert(C::kAPlanes % C::kWaves == 0, "plane k of every wave is of one kind");
   constexpr int kAK = C::kAPlanes / C::kWaves;
+  // copy sources of the expert being copied: its act rows and W2 rows
   const char* abase = (const char*)(act + (size_t)row0 * kActRowElems);
   const char* bbase = (const char*)(w2 + ((size_t)e * kH + n0) * kI);
+  int copy_exp = 0;  // its index in tile_exps
   uint32_t off[C::kPlanesPerWave];
   int dst[C::kPlanesPerWave];
 #pragma unroll
@@ -445,6 +485,15 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
     }
   }
   auto issue = [&](int s) {
+    if (s / C::kSteps != copy_exp) {  // a fused tile's next expert (wave-uniform)
+      copy_exp = s / C::kSteps;
+      uint32_t m = tile_exps;
+      for (int k = 0; k < copy_exp; ++k) m &= m - 1;
+      const int d = __builtin_ctz(m);
+      abase = (const char*)(act + (size_t)(expert_off[d] + mt * C::BM) * kActRowElems);
+      bbase = (const char*)(w2 + ((size_t)d * kH + n0) * kI);
+    }
+    s %= C::kSteps;
     char* base = lds + (s % C::kStages) * C::kStageBytes;
     // bytes per stage: bf16 hi + lo A, e4m3 B; A row blocks wholly past the
     // tile's rows are never read: no copy
@@ -458,10 +507,12 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
     }
   };
   // weight block scales of every wave's columns, staged in LDS once
-  float* wsc = (float*)(lds + C::kStages * C::kStageBytes);  // [WN][16]
-  for (int i = threadIdx.x; i < WN * kNIBlk; i += C::kThreads) {
-    const int w_n = i / kNIBlk, kb = i % kNIBlk;
-    wsc[i] = w2_scale[((size_t)e * kNHBlk + (n0 + 16 * NJ * w_n) / kBlk) * kNIBlk + kb];
+  float* wsc = (float*)(lds + C::kStages * C::kStageBytes);  // [expert of the tile][WN][16]
+  for (int i = threadIdx.x; i < n_steps / C::kSteps * WN * kNIBlk; i += C::kThreads) {
+    const int di = i / (WN * kNIBlk), w_n = (i / kNIBlk) % WN, kb = i % kNIBlk;
+    uint32_t m = tile_exps;
+    for (int k = 0; k < di; ++k) m &= m - 1;
+    wsc[i] = w2_scale[((size_t)__builtin_ctz(m) * kNHBlk + (n0 + 16 * NJ * w_n) / kBlk) * kNIBlk + kb];
   }
 
   v4f acc[MI][NJ], P[MI][NJ];
@@ -480,9 +531,9 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
   auto step = [&](int s, bool first, auto live_c) {
     constexpr int L = decltype(live_c)::value;  // live 16-row blocks of this wave
     // stages s+1 .. s+kStages-2 may stay in flight
-    wait_stages_ahead<C::kPlanesPerWave>(min(C::kSteps - 1 - s, C::kStages - 2));
+    wait_stages_ahead<C::kPlanesPerWave>(min(n_steps - 1 - s, C::kStages - 2));
     block_barrier();
-    if (s + C::kStages - 1 < C::kSteps) issue(s + C::kStages - 1);
+    if (s + C::kStages - 1 < n_steps) issue(s + C::kStages - 1);
 
     const char* sbuf = lds + (s % C::kStages) * C::kStageBytes;
     v8bf a[MI][2], al[MI][2], b[NJ][2];
@@ -510,7 +561,7 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
         P[mi][nj] = mfma_bf16_16x16x32(al[mi][1], b[nj][1], P[mi][nj]);
       }
     if (!first) {
-      const float sb = wsc[wn * kNIBlk + (s >> 1)];
+      const float sb = wsc[(s / C::kSteps * WN + wn) * kNIBlk + ((s % C::kSteps) >> 1)];
 #pragma unroll
       for (int mi = 0; mi < L; ++mi)
 #pragma unroll
@@ -527,7 +578,7 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
   // per CU, without spills.
   auto run = [&](auto live_c) {
 #pragma unroll 1
-    for (int s = 0; s < C::kSteps; s += 2) {
+    for (int s = 0; s < n_steps; s += 2) {
       step(s, true, live_c);
       step(s + 1, false, live_c);
     }
@@ -561,7 +612,7 @@ hipError_t launch_gemm2_tiled(int T, const uint8_t* w2, const float* w2_scale, c
   const int64_t blocks = ((mtiles * C::kNT + 7) / 8) * 8;
   hipLaunchKernelGGL((gemm2_tiled_kernel<WM, WN, MI, NJ, STAGES>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
                      stream, (const uint16_t*)(ws + L.act), w2, w2_scale,
-                     (const int32_t*)(ws + L.expert_off), (float*)(ws + L.down));
+                     (const int32_t*)(ws + L.expert_off), (float*)(ws + L.down), T);
   return hipGetLastError();
 }
 

@@ -37,6 +37,13 @@ static_assert(kMaxTokens * kH <= (int64_t)1 << 32, "token row offsets fit in 32 
 // Largest T for which GEMM2 also performs the weighted combine: its rows
 // never reach the workspace, and no combine pass runs.
 constexpr int kGemm2StreamMaxTokens = 64;
+// From this T on, experts that every token selects are summed inside GEMM2
+// (every_token_experts).  Below it the fused tiles (T / 64 row tiles x 28
+// column tiles, each running several experts' K loops) are too few to fill
+// the chip's 512 workgroup slots: four such experts, interleaved A/B, layer
+// us (unfused -> fused): T = 640 356 -> 388, 896 424 -> 425, 1152 553 -> 542,
+// 2048 814 -> 772, 8192 2849 -> 2712.
+constexpr int kEveryTokenFuseMinTokens = 1024;
 
 // SwiGLU activation rows (`act`) hold each fp32 value v as a pair of bf16,
 // hi = bf16(v) and lo = bf16(v - hi), so hi + lo carries v to ~2^-17
@@ -468,6 +475,28 @@ struct ExpertRows {
     return true;
   }
 };
+
+// Local experts that all T tokens select (T rows each, row begin + t being
+// token t), as a bit mask, when at least two do and T >=
+// kEveryTokenFuseMinTokens; else 0.  Their GEMM2 rows are summed per token inside
+// GEMM2 instead of in the combine: GEMM1 scales their SwiGLU rows by the
+// routing weights, a fused GEMM2 tile runs the K loop of every such expert
+// into one accumulator and writes the sum to the first one's rows, and the
+// combine adds that row once, at the first one's place in expert order.  At
+// most 8 experts (N_sel <= 8 T).  Wave-level; every kernel of a call gets the
+// same mask.
+__device__ __forceinline__ uint32_t every_token_experts(const ExpertRows& X, int T) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint32_t m = (uint32_t)__ballot(lane < kELocal && X.cnt == T);
+  static_assert(kEveryTokenFuseMinTokens > kGemm2StreamMaxTokens, "fused experts need the combine pass");
+  return (T >= kEveryTokenFuseMinTokens && __builtin_popcount(m) >= 2) ? m : 0u;
+}
+
+// The local expert whose rows hold permuted row r (< N_sel).  Wave-level.
+__device__ __forceinline__ int expert_of_row(const ExpertRows& X, int r) {
+  const int lane = threadIdx.x & (kWave - 1);
+  return __popcll(__ballot(lane < kELocal && X.o <= r)) - 1;
+}
 
 // Tile order inside the run: each L2 group (ExpertRows::tile_group) sweeps
 // all `nt` column tiles, row tile fastest, so concurrently running blocks

@@ -35,6 +35,12 @@ FUSED_COMBINE_MAX_TOKENS = 64
 # per-workgroup routing histograms (`block_hist`; kRouteSingleMaxTokens in
 # csrc/route.hip).
 ROUTE_ONE_WORKGROUP_MAX_TOKENS = 24
+# From this T on, local experts that every token selects (T rows each; at
+# least two of them) are summed inside GEMM2: their `act` rows carry the
+# routing weight, and the first one's `down` rows hold each token's weighted
+# sum over all of them (the others' `down` rows are not written)
+# (kEveryTokenFuseMinTokens in csrc/moe_common.hpp).
+EVERY_TOKEN_FUSE_MIN_TOKENS = 1024
 
 _ws_lock = threading.Lock()
 # Workspaces by (device type, device index, stream), least recently used
@@ -218,7 +224,8 @@ class RouteResult:
         self.perm_token = view(lay.perm_token, T * TOP_K, torch.int32)
         self.perm_w = view(lay.perm_w, T * TOP_K, torch.float32)
         # SwiGLU rows as bf16 (hi, lo) pairs: per 64-column chunk, 64 hi then
-        # 64 lo values (act_values() decodes them to fp32 hi + lo)
+        # 64 lo values (act_values() decodes them to fp32 hi + lo); see
+        # EVERY_TOKEN_FUSE_MIN_TOKENS for the rows of experts every token selects
         self.act = view(lay.act, T * TOP_K * 2 * I, torch.int16).view(T * TOP_K, 2 * I)
         # fp32 GEMM2 rows, in the workspace only where a combine pass reads them
         self.down = (view(lay.down, T * TOP_K * H, torch.float32).view(T * TOP_K, H)

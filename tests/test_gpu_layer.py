@@ -275,6 +275,11 @@ INTERMEDIATE_CASES = [
     ("skewed_t8192", 193, None),        # tall map, a second tall tile of 65 rows
     ("skewed_t8192", 321, 400),         # tall map, three tall tiles, the last of 65 rows
     ("prefill_t1024", 704, 400),        # tall map, partly filled tall tiles among short ones
+    # experts of every token summed inside GEMM2 (EVERY_TOKEN_FUSE_MIN_TOKENS):
+    # weights folded in by the tiled GEMM1 (T = 1024) and the wide one (T =
+    # 1100: the hot experts choose it), fused tiles with a ragged last row tile
+    ("skewed_t8192", 1024, 300),
+    ("skewed_t8192", 1100, 300),
 ]
 
 
@@ -303,6 +308,28 @@ def test_intermediates_match_oracle(pkg, orc, cuda_device, name, T, n_rows):
     act = pkg.moe.act_values(r.act[torch.as_tensor(sel, device=r.act.device)]).cpu().numpy()
     x = oracle_inputs(cfg, host, w_host)
     c_ref, o_ref = orc.expert_rows(x, perm[sel], le_all[sel])
+    # Experts that every token selects (T rows each; at least two, from
+    # EVERY_TOKEN_FUSE_MIN_TOKENS on):
+    # their act rows carry the routing weight, and the first one's GEMM2 rows
+    # hold each token's weighted sum over all of them (the others' rows are
+    # not written).
+    counts = np.diff(offs)
+    fused = np.nonzero(counts == T)[0] if T >= pkg.moe.EVERY_TOKEN_FUSE_MIN_TOKENS else np.array([], np.int64)
+    if fused.size < 2:
+        fused = np.array([], np.int64)
+    pw = r.perm_w.cpu().numpy()[:n]
+    in_fused = np.isin(le_all[sel], fused)
+    c_ref = np.where(in_fused[:, None], (c_ref * pw[sel][:, None]).astype(np.float32), c_ref)
+    if fused.size:
+        first = sel[le_all[sel] == fused[0]]  # rows of the first one: token = row - offs[first expert]
+        toks = perm[first]
+        o_sum = np.zeros((first.size, H), np.float64)
+        for d in fused:
+            rows_d = offs[d] + toks
+            o_sum += orc.expert_rows(x, toks, np.full(toks.size, d))[1].astype(np.float64) * pw[rows_d][:, None]
+        o_ref = o_ref.copy()
+        o_ref[le_all[sel] == fused[0]] = o_sum.astype(np.float32)
+        print(f"  experts of every token {fused.tolist()}: their rows checked as folded / summed")
     # act is carried as a bf16 (hi, lo) pair: fp32-level agreement (hi + lo is
     # within ~2^-17 of the fp32 value; the GEMM's fp32 summation order differs)
     ec = np.abs(act - c_ref)
@@ -314,6 +341,8 @@ def test_intermediates_match_oracle(pkg, orc, cuda_device, name, T, n_rows):
         assert r.down is None
         return  # GEMM2 rows are combined in registers, never stored
     down = r.down[torch.as_tensor(sel, device=r.down.device)].cpu().numpy()
+    written = ~in_fused | (le_all[sel] == (fused[0] if fused.size else -1))
+    down, o_ref = down[written], o_ref[written]
     eo = np.abs(down - o_ref)
     print(f"  down: max|err| {eo.max():.3e} (max|ref| {np.abs(o_ref).max():.3f})")
     bad_o = bf16_close(down, o_ref, atol=1e-4, rtol=1e-4)
