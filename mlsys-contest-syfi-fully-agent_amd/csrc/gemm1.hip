@@ -788,11 +788,10 @@ hipError_t launch_gemm1_tiled(const uint8_t* hs, const float* hs_scale, int T, c
 // ---------------------------------------------------------------------------
 // Wide path (large T): 256 rows x 256 MFMA columns per workgroup.
 //
-// With 256 x 128 tiles the kernel is bound by the L2 -> LDS feed, not by the
-// MFMAs: each CU sustains only a fixed number of outstanding L2 lines, so its
-// copy rate is capped near (lines in flight x 128 B) / L2 latency.  A 256 x 256
-// tile moves (256 + 256) x 128 B per K block for 2 x 256 x 256 x 128 FLOP, a
-// third less per FLOP than 256 x 128.
+// A 256 x 256 tile moves (256 + 256) x 128 B per K block for 2 x 256 x 256 x
+// 128 FLOP, a third less per FLOP than 256 x 128 tiles, which were slower.
+// What bounds it is the stage itself (barrier, operand reads, copy issue):
+// with every operand L2-resident (a timing-only copy) it ran only 2 % faster.
 //
 //   * 8 waves as 4 (rows) x 2 (columns); wave tile = 64 rows x (64 gate + the
 //     64 matching up columns), 4 x 8 MFMA blocks, 128 accumulator VGPRs;
