@@ -184,6 +184,33 @@ def test_layer_every_selection_local(pkg, orc, cuda_device, T, n_check):
         assert offs[32] == 8 * T and (np.diff(offs) >= 0).all()
 
 
+# Experts that every token selects, summed inside GEMM2 (EVERY_TOKEN_FUSE_MIN_TOKENS):
+# +10 on the bias of n local experts makes every token select them -- two
+# (the fewest that are fused), eight (the most: every pick of every token),
+# and with tokens ragged against the fused tiles' 64 rows.
+FORCED_CASES = [(2, 1024, None), (8, 1024, 128), (2, 3000, 256), (8, 3001, 256), (3, 1025, 256)]
+
+
+@pytest.mark.parametrize("n_forced,T,n_check", FORCED_CASES)
+def test_layer_experts_of_every_token(pkg, orc, cuda_device, n_forced, T, n_check):
+    cfg = pkg.synth.CONFIGS["prefill_t1024"]
+    off = cfg.local_expert_offset
+    w, w_host = gpu_weights(pkg, cfg.seed, cuda_device)
+    tok, host = gpu_tokens(pkg, cfg, cuda_device, T)
+    forced = off + np.arange(0, 32, 32 // n_forced)[:n_forced]
+    bias = tok[1].float()
+    bias[torch.as_tensor(forced, device=bias.device)] += 10.0
+    bias = bias.to(torch.bfloat16)
+    tok = (tok[0], bias, tok[2], tok[3])
+    host = (host[0], bias.view(torch.int16).cpu().numpy().view(np.uint16), host[2], host[3])
+    ref_ids, _ = orc.route(host[0], host[1], cfg.routed_scaling_factor)
+    assert np.isin(forced, ref_ids).all() and all(np.isin(forced, row).all() for row in ref_ids[:64])
+    print(f"layer forced-experts case n={n_forced} T={T}", flush=True)
+    check_layer(pkg, orc, cuda_device, cfg, off, tok, host, w, w_host, n_check)
+    offs = pkg.intermediates(pkg.workspace(cuda_device, T), T).expert_off.cpu().numpy()
+    assert (np.diff(offs)[forced - off] == T).all()
+
+
 def _random_cases(n, seed):
     """(routing config, T, window offset, token seed, weight seed, rsf) drawn
     from a fixed generator: T over every kernel path, any window start in
