@@ -5,7 +5,9 @@
 //     (what the layer's HBM-bound kernels do with the expert weights);
 //   * MFMA issue rate: independent accumulator chains of the two instructions
 //     the GEMMs use (v_mfma_f32_16x16x128_f8f6f4 and v_mfma_f32_16x16x32_bf16),
-//     operands in registers, launched by bench.py at 16 waves per CU;
+//     operands in registers, launched by bench.py at 16 waves per CU; once
+//     with fixed operands and once with random ones, whose switching power
+//     lowers the clock the chip sustains;
 //   * trace markers: two empty kernels whose dispatches split a kernel trace
 //     of several workloads' calls into per-workload spans.
 #include <hip/hip_runtime.h>
@@ -78,6 +80,63 @@ __global__ void __launch_bounds__(512) mfma_bf16_loop(int iters, float* __restri
   sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// Random operands: four register sets per wave from an integer hash of the
+// thread and set index, chain j multiplying set j % 4 by set (j + 1) % 4, so
+// consecutive MFMAs see different bits, as a GEMM's operands do.  e4m3 bytes
+// are masked to 0x77 (finite, |x| < 1.5 * 2^7); bf16 values lie in [-1, 1).
+__device__ __forceinline__ uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x21f0aaadU;
+  x ^= x >> 15;
+  x *= 0xd35a2d97U;
+  x ^= x >> 15;
+  return x;
+}
+constexpr int kSets = 4;
+
+__global__ void __launch_bounds__(512) mfma_f8_loop_random(int iters, float* __restrict__ sink) {
+  const uint32_t g = blockIdx.x * 512u + threadIdx.x;
+  v8i a[kSets], b[kSets];
+#pragma unroll
+  for (int j = 0; j < kSets; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[j][i] = (int)(mix32(g * 64u + 8u * j + i) & 0x77777777u);
+      b[j][i] = (int)(mix32(g * 64u + 32u + 8u * j + i) & 0x77777777u);
+    }
+  v4f acc[kChains] = {};
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int j = 0; j < kChains; ++j)
+      acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a[j % kSets], b[(j + 1) % kSets], acc[j], 0, 0, 0,
+                                                                 0, 0, 0);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kChains; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  sink[g] = s;
+}
+
+__global__ void __launch_bounds__(512) mfma_bf16_loop_random(int iters, float* __restrict__ sink) {
+  const uint32_t g = blockIdx.x * 512u + threadIdx.x;
+  v8bf a[kSets], b[kSets];
+#pragma unroll
+  for (int j = 0; j < kSets; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[j][i] = (__bf16)((float)(mix32(g * 64u + 8u * j + i) & 0xFFFFu) * (1.0f / 32768.0f) - 1.0f);
+      b[j][i] = (__bf16)((float)(mix32(g * 64u + 32u + 8u * j + i) & 0xFFFFu) * (1.0f / 32768.0f) - 1.0f);
+    }
+  v4f acc[kChains] = {};
+  for (int it = 0; it < iters; ++it)
+#pragma unroll
+    for (int j = 0; j < kChains; ++j)
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j % kSets], b[(j + 1) % kSets], acc[j], 0, 0, 0);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kChains; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  sink[g] = s;
+}
+
 __global__ void trace_mark_begin() {}
 __global__ void trace_mark_end() {}
 
@@ -94,14 +153,21 @@ int moe_bench_read_stream(const void* src, size_t bytes, void* sink, int blocks,
   return (int)hipGetLastError();
 }
 
-// kind 0: fp8 f8f6f4 16x16x128, kind 1: bf16 16x16x32.  `blocks` workgroups
+// kind 0: fp8 f8f6f4 16x16x128, kind 1: bf16 16x16x32, fixed operands;
+// kinds 2 and 3: the same with random operands.  `blocks` workgroups
 // of 512 threads, each wave `iters` x 8 MFMAs; `sink` holds blocks * 512
 // floats.  FLOPs = blocks * 8 waves * iters * 8 * (2 * 16 * 16 * K).
 int moe_bench_mfma_loop(int kind, int iters, int blocks, void* sink, hipStream_t stream) {
   if (kind == 0)
     hipLaunchKernelGGL(mfma_f8_loop, dim3(blocks), dim3(512), 0, stream, iters, (float*)sink);
-  else
+  else if (kind == 1)
     hipLaunchKernelGGL(mfma_bf16_loop, dim3(blocks), dim3(512), 0, stream, iters, (float*)sink);
+  else if (kind == 2)
+    hipLaunchKernelGGL(mfma_f8_loop_random, dim3(blocks), dim3(512), 0, stream, iters, (float*)sink);
+  else if (kind == 3)
+    hipLaunchKernelGGL(mfma_bf16_loop_random, dim3(blocks), dim3(512), 0, stream, iters, (float*)sink);
+  else
+    return (int)hipErrorInvalidValue;
   return (int)hipGetLastError();
 }
 
