@@ -493,6 +493,8 @@ gemm2_tiled_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__
       abase = (const char*)(act + (size_t)(expert_off[d] + mt * C::BM) * kActRowElems);
       bbase = (const char*)(w2 + ((size_t)d * kH + n0) * kI);
     }
+    // the buffer of global step s is s % kStages, as step() reads it
+    static_assert(C::kSteps % C::kStages == 0, "an expert's step count keeps the ring position");
     s %= C::kSteps;
     char* base = lds + (s % C::kStages) * C::kStageBytes;
     // bytes per stage: bf16 hi + lo A, e4m3 B; A row blocks wholly past the
