@@ -135,6 +135,17 @@ def test_synth_validation_without_gpu(pkg):
     assert S.moe_synth_bias(0, None, 9, 0.0, ctypes.c_void_p(16), None) == -1
 
 
+def test_bench_probe_validation_without_gpu(pkg):
+    """The roofline probes (lib/libmoe_bench.so) refuse what they cannot run
+    before launching: an MFMA kind other than 0-3, a read size that the
+    workgroups do not split evenly (hipErrorInvalidValue = 1)."""
+    B = pkg._lib.bench_lib()
+    assert B.moe_bench_mfma_loop(4, 1, 1, None, None) == 1
+    assert B.moe_bench_mfma_loop(-1, 1, 1, None, None) == 1
+    assert B.moe_bench_read_stream(None, 4096, None, 1, None) == 1
+    assert B.moe_bench_read_stream(None, 1 << 20, None, 0, None) == 1
+
+
 def test_python_entry_rejects_bad_shapes(pkg):
     import torch
 
