@@ -47,10 +47,15 @@ combine_kernel(const float* __restrict__ down, const int32_t* __restrict__ pair_
   }
   // Experts of every token (every_token_experts): GEMM2 wrote the token's
   // weighted sum over them to the first one's row; add that row once, with
-  // weight 1, at its place in expert order, and skip the others' rows.
+  // weight 1, at its place in expert order, and skip the others' rows.  The
+  // row loads wait for this test (the offsets' read costs the pass ~0.4 us
+  // at T = 1024), so below the size where it can hold they are not read.
   ExpertRows X;
-  X.load(expert_off);
-  const uint32_t fused = every_token_experts(X, T);
+  uint32_t fused = 0u;
+  if (T >= kEveryTokenFuseMinTokens) {  // kernel-uniform
+    X.load(expert_off);
+    fused = every_token_experts(X, T);
+  }
   if (fused) {
 #pragma unroll
     for (int k = 0; k < kTopK; ++k) {
